@@ -1,0 +1,69 @@
+"""Build libssd_mi355x.so for gfx950 from csrc/*.hip with hipcc.
+
+    python dhammic-ai_amd/build.py [--jobs N] [--verbose]
+
+Objects go to dhammic-ai_amd/_build/, the library to
+dhammic-ai_amd/kernels/libssd_mi355x.so (in-tree, so it travels with the
+source tree to the GPU box).
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "kernels" / "libssd_mi355x.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-parameter",
+    # packed fp32 VALU ops are kept out of every kernel on this pool
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{PKG.parent / 'include'}",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(str(c) for c in cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(map(str, cmd))}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def build(jobs: int = 8, verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    objs = [BUILD / (s.stem + ".o") for s in sources]
+
+    def compile_one(pair):
+        src, obj = pair
+        _run([HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)], verbose)
+
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(compile_one, zip(sources, objs)))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--verbose", action="store_true")
+    a = ap.parse_args()
+    path = build(a.jobs, a.verbose)
+    print(f"built {path}")
+    sys.exit(0)

@@ -1,0 +1,300 @@
+// extern "C" entry points: validation, workspace layout, launch sequences.
+#include <string.h>
+
+#include "../../include/ssd_mi355x.h"
+#include "ssd_launch.h"
+
+namespace {
+
+constexpr size_t kAlign = 256;
+constexpr size_t kMaxLds = 160 * 1024;   // LDS per workgroup on gfx950
+constexpr int kMaxSeq = 16000;           // chunk-table prefix kept in LDS
+constexpr int kMaxGrid = 65535;          // grid.y / grid.z limit used by the launches
+constexpr int kNormMaxHP = 16384;        // dw partial row kept in LDS
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Plan {
+  SsdDims d;
+  int dtype, state_dtype;
+  int64_t nslices, hslice, npass_blk, norm_blocks;
+  // byte offsets inside each workspace
+  size_t o_chunks, o_seq0, o_cs, o_hin, o_ypre, o_rstd, saved_bytes;
+  size_t o_st, fwd_bytes;
+  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, bwd_bytes;
+};
+
+int plan(const ssd_desc_t* s, Plan* p) {
+  if (!s || !p) return SSD_ERR_INVALID;
+  memset(p, 0, sizeof(*p));
+  if (s->batch < 1 || s->seqlen < 1 || s->nheads < 1 || s->headdim < 1 || s->ngroups < 1 || s->dstate < 1 ||
+      s->chunk < 1)
+    return SSD_ERR_INVALID;
+  if (s->nheads % s->ngroups) return SSD_ERR_INVALID;
+  if ((s->dtype != SSD_DTYPE_F32 && s->dtype != SSD_DTYPE_BF16) ||
+      (s->state_dtype != SSD_DTYPE_F32 && s->state_dtype != SSD_DTYPE_BF16))
+    return SSD_ERR_INVALID;
+  if (s->a_mode != SSD_A_PER_HEAD && s->a_mode != SSD_A_PER_TOKEN && s->a_mode != SSD_A_CUMSUM)
+    return SSD_ERR_INVALID;
+  if (s->a_mode != SSD_A_PER_HEAD && s->has_dt) return SSD_ERR_INVALID;
+  if (s->varlen && (s->batch != 1 || s->nseq < 1)) return SSD_ERR_INVALID;
+  if ((s->a_mode == SSD_A_CUMSUM || s->want_A_cumsum) && (s->varlen || s->seqlen % s->chunk)) return SSD_ERR_INVALID;
+  if (s->has_z && !(s->norm_eps >= 0.0f)) return SSD_ERR_INVALID;
+  if (s->chunk > SSD_MAX_CHUNK || s->headdim > SSD_MAX_HEADDIM || s->dstate > SSD_MAX_DSTATE)
+    return SSD_ERR_UNSUPPORTED;
+  if (s->varlen && s->nseq > kMaxSeq) return SSD_ERR_UNSUPPORTED;
+  const int64_t R = s->batch * s->seqlen;
+  if (R > INT32_MAX / 2 || s->nheads > kMaxGrid) return SSD_ERR_UNSUPPORTED;
+  const int64_t cps = (s->seqlen + s->chunk - 1) / s->chunk;
+  const int64_t nseq = s->varlen ? s->nseq : s->batch;
+  const int64_t max_chunks = s->varlen ? cps + nseq : s->batch * cps;
+  if (max_chunks > kMaxGrid) return SSD_ERR_UNSUPPORTED;
+  if (s->has_z && s->nheads * s->headdim > kNormMaxHP) return SSD_ERR_UNSUPPORTED;
+
+  SsdDims& d = p->d;
+  d.batch = (int)s->batch; d.seqlen = (int)s->seqlen; d.H = (int)s->nheads; d.P = (int)s->headdim;
+  d.G = (int)s->ngroups; d.N = (int)s->dstate; d.Q = (int)s->chunk;
+  d.Ppad = round_up(d.P, 32); d.Npad = round_up(d.N, 32); d.Qpad = round_up(d.Q, SSD_BLK);
+  d.nseq = (int)nseq; d.max_chunks = (int)max_chunks; d.hpg = d.H / d.G; d.R = R;
+  d.a_mode = s->a_mode; d.has_dt = s->has_dt != 0; d.has_D = s->has_D != 0; d.has_z = s->has_z != 0;
+  d.has_init = s->has_init != 0; d.has_dfinal = s->has_dfinal != 0; d.varlen = s->varlen != 0;
+  d.eps = s->norm_eps;
+  p->dtype = s->dtype;
+  p->state_dtype = s->state_dtype;
+  if (lds_chunk_scan_fwd(p->dtype, d) > kMaxLds || lds_bwd_col(p->dtype, d) > kMaxLds ||
+      lds_bwd_row(p->dtype, d) > kMaxLds)
+    return SSD_ERR_UNSUPPORTED;
+
+  // head slices of the backward: enough blocks to fill the chip, fewest partials
+  const int64_t per_slice = max_chunks * d.G * (d.Qpad / SSD_BLK);
+  int64_t ns = (2048 + per_slice - 1) / per_slice;
+  if (ns < 1) ns = 1;
+  if (ns > d.hpg) ns = d.hpg;
+  p->hslice = (d.hpg + ns - 1) / ns;
+  p->nslices = (d.hpg + p->hslice - 1) / p->hslice;
+  p->npass_blk = ((int64_t)d.Ppad * d.Npad + SSD_PASS_THREADS - 1) / SSD_PASS_THREADS;
+  p->norm_blocks = R < 1024 ? R : 1024;
+
+  const size_t es = p->dtype == SSD_DTYPE_BF16 ? 2 : 4;
+  const size_t MC = (size_t)max_chunks, H = (size_t)d.H, PN = (size_t)d.Ppad * d.Npad;
+  size_t off = 0;
+  auto take = [&off](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+  p->o_chunks = take(MC * sizeof(ChunkInfo));
+  p->o_seq0 = take((nseq + 1) * sizeof(int32_t));
+  p->o_cs = take(MC * H * d.Qpad * sizeof(float));
+  p->o_hin = take(MC * H * PN * es);
+  p->o_ypre = d.has_z ? take((size_t)R * H * d.P * es) : 0;
+  p->o_rstd = d.has_z ? take((size_t)R * sizeof(float)) : 0;
+  p->saved_bytes = off;
+  off = 0;
+  p->o_st = take(MC * H * PN * sizeof(float));
+  p->fwd_bytes = off;
+  off = 0;
+  p->o_dyp = d.has_z ? take((size_t)R * H * d.P * es) : 0;
+  p->o_dst = take(MC * H * PN * sizeof(float));
+  p->o_dtot = take(MC * H * p->npass_blk * sizeof(float));
+  p->o_rowG = take(MC * H * d.Qpad * sizeof(float));
+  p->o_colG = take(MC * H * d.Qpad * sizeof(float));
+  p->o_eterm = take(MC * H * d.Qpad * sizeof(float));
+  p->o_dcs = take(MC * H * d.Qpad * sizeof(float));
+  p->o_xdx = take(MC * H * d.Qpad * sizeof(float));
+  p->o_dD = take(MC * H * (d.Qpad / SSD_BLK) * sizeof(float));
+  p->o_dA = take(MC * H * sizeof(float));
+  const size_t bcn = (size_t)R * d.G * d.N * sizeof(float);
+  p->o_dBp = p->nslices > 1 ? take(p->nslices * bcn) : 0;
+  p->o_dCp = p->nslices > 1 ? take(p->nslices * bcn) : 0;
+  p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
+  p->bwd_bytes = off;
+  return SSD_OK;
+}
+
+void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
+  unsigned char* s = static_cast<unsigned char*>(saved);
+  b->chunks = reinterpret_cast<ChunkInfo*>(s + p.o_chunks);
+  b->seq_chunk0 = reinterpret_cast<int32_t*>(s + p.o_seq0);
+  b->cs = reinterpret_cast<float*>(s + p.o_cs);
+  b->hin = s + p.o_hin;
+  b->ypre = p.d.has_z ? s + p.o_ypre : nullptr;
+  b->rstd = p.d.has_z ? reinterpret_cast<float*>(s + p.o_rstd) : nullptr;
+  b->npass_blk = (int)p.npass_blk;
+  b->nslices = (int)p.nslices;
+  b->hslice = (int)p.hslice;
+  b->norm_blocks = (int)p.norm_blocks;
+}
+
+void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
+  unsigned char* s = static_cast<unsigned char*>(scratch);
+  b->dyp = p.d.has_z ? s + p.o_dyp : nullptr;
+  b->dst = reinterpret_cast<float*>(s + p.o_dst);
+  b->dtot_part = reinterpret_cast<float*>(s + p.o_dtot);
+  b->rowG = reinterpret_cast<float*>(s + p.o_rowG);
+  b->colG = reinterpret_cast<float*>(s + p.o_colG);
+  b->eterm = reinterpret_cast<float*>(s + p.o_eterm);
+  b->dcs_off = reinterpret_cast<float*>(s + p.o_dcs);
+  b->xdx = reinterpret_cast<float*>(s + p.o_xdx);
+  b->dD_part = reinterpret_cast<float*>(s + p.o_dD);
+  b->dA_part = reinterpret_cast<float*>(s + p.o_dA);
+  b->dB_part = p.nslices > 1 ? reinterpret_cast<float*>(s + p.o_dBp) : nullptr;
+  b->dC_part = p.nslices > 1 ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
+  b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
+}
+
+#define SSD_TRY(expr)                          \
+  do {                                         \
+    if ((expr) != hipSuccess) return SSD_ERR_HIP; \
+  } while (0)
+
+// Brackets the launches of one phase with the caller's events (if any).
+struct PhaseTimer {
+  void* const* ev;
+  hipStream_t s;
+  hipError_t begin(int ph) const {
+    return ev ? hipEventRecord(static_cast<hipEvent_t>(ev[2 * ph]), s) : hipSuccess;
+  }
+  hipError_t end(int ph) const {
+    return ev ? hipEventRecord(static_cast<hipEvent_t>(ev[2 * ph + 1]), s) : hipSuccess;
+  }
+};
+
+#define SSD_PHASE(tm, ph, expr)   \
+  do {                            \
+    SSD_TRY((tm).begin(ph));      \
+    SSD_TRY(expr);                \
+    SSD_TRY((tm).end(ph));        \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int ssd_validate(const ssd_desc_t* desc) {
+  Plan p;
+  return plan(desc, &p);
+}
+
+size_t ssd_workspace_bytes(const ssd_desc_t* desc, int kind) {
+  Plan p;
+  if (plan(desc, &p) != SSD_OK) return 0;
+  switch (kind) {
+    case SSD_WS_SAVED: return p.saved_bytes;
+    case SSD_WS_FWD_SCRATCH: return p.fwd_bytes;
+    case SSD_WS_BWD_SCRATCH: return p.bwd_bytes;
+    default: return 0;
+  }
+}
+
+int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t saved_bytes, void* scratch,
+            size_t scratch_bytes, void* stream) {
+  Plan p;
+  int st = plan(desc, &p);
+  if (st != SSD_OK) return st;
+  const SsdDims& d = p.d;
+  if (!a || !a->x || !a->A || !a->B || !a->C || !a->y) return SSD_ERR_INVALID;
+  if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight)) ||
+      (d.has_init && !a->init) || (d.varlen && !a->cu_seqlens) || (desc->want_final && !a->final_state) ||
+      (desc->want_A_cumsum && !a->A_cumsum_out))
+    return SSD_ERR_INVALID;
+  if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.fwd_bytes) return SSD_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SsdBufs b;
+  memset(&b, 0, sizeof(b));
+  bind_saved(p, saved, &b);
+  b.st = reinterpret_cast<float*>(scratch);
+  SsdIn in = {a->x, a->dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
+  const PhaseTimer tm{a->events, s};
+  SSD_PHASE(tm, SSD_PH_CHUNK_TABLE, launch_chunk_table(d, b, a->cu_seqlens, s));
+  SSD_PHASE(tm, SSD_PH_CUMSUM,
+            launch_chunk_cumsum(p.dtype, d, b, a->A, a->dt, desc->want_A_cumsum ? a->A_cumsum_out : nullptr, s));
+  SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, a->dt, b.st, s));
+  SSD_PHASE(tm, SSD_PH_FWD_PASS,
+            launch_state_pass_fwd(p.dtype, p.state_dtype, d, b, d.has_init ? a->init : nullptr,
+                                  desc->want_final ? a->final_state : nullptr, s));
+  SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, d.has_z ? b.ypre : a->y, s));
+  if (d.has_z) SSD_PHASE(tm, SSD_PH_NORM_FWD, launch_gated_norm_fwd(p.dtype, d, b, in, a->y, s));
+  return SSD_OK;
+}
+
+int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, size_t saved_bytes, void* scratch,
+            size_t scratch_bytes, void* stream) {
+  Plan p;
+  int st = plan(desc, &p);
+  if (st != SSD_OK) return st;
+  const SsdDims& d = p.d;
+  if (!a || !a->x || !a->A || !a->B || !a->C || !a->dy || !a->dx || !a->dB || !a->dC) return SSD_ERR_INVALID;
+  if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight || !a->dz)) ||
+      (d.varlen && !a->cu_seqlens) || (d.has_dfinal && !a->dfinal))
+    return SSD_ERR_INVALID;
+  if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.bwd_bytes) return SSD_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SsdBufs b;
+  memset(&b, 0, sizeof(b));
+  bind_saved(p, const_cast<void*>(saved), &b);
+  bind_bwd(p, scratch, &b);
+  SsdIn in = {a->x, a->dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
+  const PhaseTimer tm{a->events, s};
+  const void* dY = a->dy;
+  if (d.has_z) {
+    SSD_PHASE(tm, SSD_PH_NORM_BWD, launch_gated_norm_bwd(p.dtype, d, b, in, a->dy, a->dz, s));
+    if (a->dnorm_weight)
+      SSD_PHASE(tm, SSD_PH_NORM_DW, launch_reduce_rows((int)p.norm_blocks, d.H * d.P, b.dw_part, a->dnorm_weight, s));
+    dY = b.dyp;
+  }
+  SSD_PHASE(tm, SSD_PH_BWD_STATE, launch_chunk_state(p.dtype, 1, d, b, dY, a->C, a->dt, b.dst, s));
+  SSD_PHASE(tm, SSD_PH_BWD_PASS,
+            launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
+                                  d.has_init ? a->dinit : nullptr, s));
+  SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));
+  SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, d, b, in, dY, a->dC, s));
+  SSD_PHASE(tm, SSD_PH_BWD_FINISH,
+            launch_bwd_finish(p.dtype, d, b, in, d.has_dt ? a->ddt : nullptr,
+                              d.a_mode == SSD_A_PER_TOKEN ? a->dA : nullptr, s));
+  if (p.nslices > 1) {
+    const int64_t nelem = d.R * d.G * d.N;
+    SSD_TRY(tm.begin(SSD_PH_BWD_REDUCE_BC));
+    SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dB_part, a->dB, s));
+    SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dC_part, a->dC, s));
+    SSD_TRY(tm.end(SSD_PH_BWD_REDUCE_BC));
+  }
+  float* dA_head = d.a_mode == SSD_A_PER_HEAD ? reinterpret_cast<float*>(a->dA) : nullptr;
+  float* dD = d.has_D ? a->dD : nullptr;
+  if (dA_head || dD) SSD_PHASE(tm, SSD_PH_BWD_REDUCE_HEADS, launch_reduce_heads(d, b, dA_head, dD, s));
+  return SSD_OK;
+}
+
+int ssd_materialize_L(const ssd_desc_t* desc, const void* a, void* L, void* stream) {
+  if (!desc || !a || !L) return SSD_ERR_INVALID;
+  if (desc->batch < 1 || desc->seqlen < 1 || desc->nheads < 1 || desc->chunk < 1 || desc->seqlen % desc->chunk ||
+      desc->varlen || (desc->dtype != SSD_DTYPE_F32 && desc->dtype != SSD_DTYPE_BF16))
+    return SSD_ERR_INVALID;
+  if (desc->batch * desc->nheads * (desc->seqlen / desc->chunk) > INT32_MAX) return SSD_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SSD_TRY(launch_materialize_L(desc->dtype, (int)desc->batch, (int)desc->seqlen, (int)desc->nheads,
+                               (int)desc->chunk, a, L, s));
+  return SSD_OK;
+}
+
+int ssd_decay_chunk(const ssd_desc_t* desc, const void* A_cumsum, void* decay_chunk, void* stream) {
+  if (!desc || !A_cumsum || !decay_chunk) return SSD_ERR_INVALID;
+  if (desc->batch < 1 || desc->seqlen < 1 || desc->nheads < 1 || desc->chunk < 1 || desc->seqlen % desc->chunk ||
+      desc->varlen || (desc->dtype != SSD_DTYPE_F32 && desc->dtype != SSD_DTYPE_BF16))
+    return SSD_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SSD_TRY(launch_decay_chunk(desc->dtype, (int)desc->batch, (int)desc->nheads, (int)(desc->seqlen / desc->chunk),
+                             (int)desc->chunk, A_cumsum, decay_chunk, s));
+  return SSD_OK;
+}
+
+const char* ssd_status_string(int status) {
+  switch (status) {
+    case SSD_OK: return "ok";
+    case SSD_ERR_INVALID: return "invalid argument";
+    case SSD_ERR_UNSUPPORTED: return "unsupported shape or option";
+    case SSD_ERR_WORKSPACE: return "workspace missing or too small";
+    case SSD_ERR_HIP: return "HIP launch error";
+    default: return "unknown status";
+  }
+}
+
+int ssd_abi_version(void) { return 1; }
+
+}  // extern "C"

@@ -1,0 +1,69 @@
+// Host-side launchers of the SSD kernels (one per kernel family; each
+// dispatches on the storage dtype, 0 = fp32, 1 = bf16). All return the
+// hipError_t of their launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ssd_params.h"
+
+// Lift the default dynamic-LDS cap for kernels that stage more than 64 KiB
+// (gfx950 offers 160 KiB per workgroup).
+template <typename K>
+inline void ensure_lds(K kernel, size_t bytes) {
+  if (bytes > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)bytes);
+}
+
+struct SsdIn {
+  const void* x; const float* dt; const void* A; const void* B; const void* C;
+  const float* D; const void* z; const float* w; const void* init; const int32_t* cu;
+};
+
+// ssd_prep.hip
+hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t* cu, hipStream_t s);
+hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, const void* A,
+                               const float* dt, void* A_cumsum_out, hipStream_t s);
+hipError_t launch_decay_chunk(int dtype, int batch, int H, int nch, int Q, const void* Acs,
+                              void* out, hipStream_t s);
+hipError_t launch_materialize_L(int dtype, int batch, int seqlen, int H, int Q, const void* a,
+                                void* L, hipStream_t s);
+
+// ssd_state.hip
+// mode 0: st[c][h] = sum_l x_l^T (exp(cs_last - cs_l) dt_l B_l)      (forward chunk states)
+// mode 1: dst[c][h] = sum_l dy_l^T (exp(cs_l) C_l)                    (backward local dh)
+hipError_t launch_chunk_state(int dtype, int mode, const SsdDims& d, const SsdBufs& b,
+                              const void* U, const void* V, const float* dt, float* out, hipStream_t s);
+hipError_t launch_state_pass_fwd(int dtype, int state_dtype, const SsdDims& d, const SsdBufs& b,
+                                 const void* init, void* final_state, hipStream_t s);
+hipError_t launch_state_pass_bwd(int dtype, int state_dtype, const SsdDims& d, const SsdBufs& b,
+                                 const void* dfinal, void* dinit, hipStream_t s);
+
+// ssd_scan_fwd.hip
+hipError_t launch_chunk_scan_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                                 void* y, hipStream_t s);
+size_t lds_chunk_scan_fwd(int dtype, const SsdDims& d);
+
+// ssd_bwd.hip
+hipError_t launch_bwd_col(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                          const void* dy, void* dx, void* dB, hipStream_t s);
+hipError_t launch_bwd_row(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                          const void* dy, void* dC, hipStream_t s);
+hipError_t launch_bwd_finish(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                             float* ddt, void* dA_tok, hipStream_t s);
+size_t lds_bwd_col(int dtype, const SsdDims& d);
+size_t lds_bwd_row(int dtype, const SsdDims& d);
+
+// ssd_norm.hip
+hipError_t launch_gated_norm_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                                 void* y, hipStream_t s);
+hipError_t launch_gated_norm_bwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
+                                 const void* dout, void* dz, hipStream_t s);
+
+// ssd_reduce.hip
+hipError_t launch_reduce_slices(int dtype, int64_t nelem, int nslices, const float* part, void* out,
+                                hipStream_t s);
+hipError_t launch_reduce_heads(const SsdDims& d, const SsdBufs& b, float* dA_head, float* dD,
+                               hipStream_t s);
+hipError_t launch_reduce_rows(int nblocks, int width, const float* part, float* out, hipStream_t s);

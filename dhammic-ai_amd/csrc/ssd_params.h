@@ -1,0 +1,48 @@
+// Launch parameters shared by the host entry points and the kernels.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ssd_common.h"
+
+// Rows of the token axis per block tile inside a chunk.
+#define SSD_BLK 64
+
+struct SsdDims {
+  int batch, seqlen, H, P, G, N, Q;  // Q: tokens per chunk
+  int Ppad, Npad, Qpad;              // P, N rounded up to 32; Q rounded up to 64
+  int nseq, max_chunks, hpg;         // hpg: heads per group
+  int64_t R;                         // rows of the packed token axis (batch * seqlen)
+  int a_mode, has_dt, has_D, has_z, has_init, has_dfinal, varlen;
+  float eps;
+};
+
+// Internal buffers (all inside the caller's workspaces).
+struct SsdBufs {
+  ChunkInfo* chunks;       // [max_chunks]
+  int32_t* seq_chunk0;     // [nseq + 1] first chunk of each sequence
+  float* cs;               // [max_chunks][H][Qpad] in-chunk inclusive cumsum of a
+  void* hin;               // [max_chunks][H][Ppad][Npad] (T) state entering each chunk
+  void* ypre;              // [R][H][P] (T) y before the gated norm (has_z)
+  float* rstd;             // [R] (has_z)
+  float* st;               // fwd scratch: [max_chunks][H][Ppad][Npad] chunk-local states
+  // backward scratch
+  void* dyp;               // [R][H][P] (T) gradient at y before the gated norm (has_z)
+  float* dst;              // [max_chunks][H][Ppad][Npad] local dh, then gradient leaving each chunk
+  float* dtot_part;        // [max_chunks][H][npass_blk]
+  float* rowG;             // [max_chunks][H][Qpad]
+  float* colG;             // [max_chunks][H][Qpad]
+  float* eterm;            // [max_chunks][H][Qpad]
+  float* dcs_off;          // [max_chunks][H][Qpad]
+  float* xdx;              // [max_chunks][H][Qpad]
+  float* dD_part;          // [max_chunks][H][Qpad/64]
+  float* dA_part;          // [max_chunks][H]
+  float* dB_part;          // [nslices][R][G][N]
+  float* dC_part;          // [nslices][R][G][N]
+  float* dw_part;          // [norm_blocks][H*P]
+  int npass_blk, nslices, hslice, norm_blocks;
+};
+
+// Elements per thread block in the state passes.
+#define SSD_PASS_THREADS 256

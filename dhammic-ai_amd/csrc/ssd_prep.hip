@@ -1,0 +1,223 @@
+// Chunk table, in-chunk cumsum of the log-decay, and the reference cache
+// tensors (L, decay_chunk).
+#include "ssd_launch.h"
+
+// ---------------------------------------------------------------------------
+// Chunk table: chunks restart at every sequence start, so each chunk lies in
+// one sequence (the reference pads every sequence to a chunk multiple,
+// r2/dhammic-ai/src/mamba_base_engine.py:154-165). One block; the per-sequence
+// prefix lives in LDS (nseq <= 16000 is checked on the host).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_chunk_table(const int32_t* __restrict__ cu, int nseq, int seqlen,
+                                                     int Q, int max_chunks, ChunkInfo* __restrict__ chunks,
+                                                     int32_t* __restrict__ seq_chunk0) {
+  extern __shared__ int32_t s_first[];  // [nseq + 1]
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int s = 0; s < nseq; ++s) {
+      int start, end;
+      if (cu) {
+        start = min(max(cu[s], 0), seqlen);
+        end = min(max(cu[s + 1], start), seqlen);
+      } else {
+        start = s * seqlen;
+        end = start + seqlen;
+      }
+      // clamped so that malformed offsets can never index past the table
+      s_first[s] = min(acc, max_chunks);
+      acc += (end - start + Q - 1) / Q;
+    }
+    s_first[nseq] = min(acc, max_chunks);
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s <= nseq; s += blockDim.x) seq_chunk0[s] = s_first[s];
+  const int total = s_first[nseq];
+  for (int c = threadIdx.x; c < max_chunks; c += blockDim.x) {
+    ChunkInfo ci;
+    ci.row0 = 0; ci.len = 0; ci.seq = -1; ci.idx_in_seq = 0;
+    if (c < total) {
+      int lo = 0, hi = nseq - 1;  // last s with s_first[s] <= c
+      while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (s_first[mid] <= c) lo = mid; else hi = mid - 1;
+      }
+      int start, end;
+      if (cu) {
+        start = min(max(cu[lo], 0), seqlen);
+        end = min(max(cu[lo + 1], start), seqlen);
+      } else {
+        start = lo * seqlen;
+        end = start + seqlen;
+      }
+      const int k = c - s_first[lo];
+      ci.row0 = start + k * Q;
+      ci.len = min(Q, end - ci.row0);
+      ci.seq = lo;
+      ci.idx_in_seq = k;
+    }
+    chunks[c] = ci;
+  }
+}
+
+hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t* cu, hipStream_t s) {
+  const int seqlen = d.varlen ? (int)d.R : d.seqlen;
+  hipLaunchKernelGGL(k_chunk_table, dim3(1), dim3(256), (d.nseq + 1) * sizeof(int32_t), s,
+                     d.varlen ? cu : nullptr, d.nseq, seqlen, d.Q, d.max_chunks, b.chunks, b.seq_chunk0);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// In-chunk inclusive cumsum of a (ssd_scan.py:364-368), one wave per
+// (chunk, head), fp32. Positions past the chunk's length carry a = 0, so
+// cs[Qpad-1] is the chunk total. Optionally writes the reference's
+// A_cumsum (b, h, c, Q) in the input dtype.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo* __restrict__ chunks,
+                                                      const void* __restrict__ Av, const float* __restrict__ dt,
+                                                      float* __restrict__ cs, T* __restrict__ acs_out) {
+  const int c = blockIdx.x;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = lane_id();
+  if (h >= d.H) return;
+  const ChunkInfo ci = chunks[c];
+  if (ci.len == 0) return;
+  const int per = d.Qpad / 64;  // 1, 2 or 4 consecutive positions per lane
+  float v[4];
+  float run = 0.0f;
+  for (int e = 0; e < per; ++e) {
+    const int l = lane * per + e;
+    float a = 0.0f;
+    if (d.a_mode == 2) {
+      // the caller's inclusive cumsum: differences are not needed, keep it as is
+      const int nch = d.seqlen / d.Q;
+      const T* A = reinterpret_cast<const T*>(Av);
+      const int ll = min(l, ci.len - 1);
+      v[e] = to_f(A[(((int64_t)ci.seq * d.H + h) * nch + ci.idx_in_seq) * d.Q + ll]);
+      continue;
+    }
+    if (l < ci.len) {
+      const int64_t row = ci.row0 + l;
+      if (d.a_mode == 0) {
+        const float* A = reinterpret_cast<const float*>(Av);
+        a = (d.has_dt ? dt[row * d.H + h] : 1.0f) * A[h];
+      } else {
+        const T* A = reinterpret_cast<const T*>(Av);
+        a = to_f(A[row * d.H + h]);
+      }
+    }
+    run += a;
+    v[e] = run;
+  }
+  if (d.a_mode != 2) {
+    // exclusive scan of the lane totals across the wave
+    float incl = run;
+    for (int off = 1; off < 64; off <<= 1) {
+      float o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    const float excl = incl - run;
+    for (int e = 0; e < per; ++e) v[e] += excl;
+  }
+  float* out = cs + ((int64_t)c * d.H + h) * d.Qpad;
+  for (int e = 0; e < per; ++e) out[lane * per + e] = v[e];
+  if (acs_out) {
+    const int nch = d.seqlen / d.Q;
+    T* o = acs_out + (((int64_t)ci.seq * d.H + h) * nch + ci.idx_in_seq) * d.Q;
+    for (int e = 0; e < per; ++e) {
+      const int l = lane * per + e;
+      if (l < d.Q) o[l] = from_f<T>(v[e]);
+    }
+  }
+}
+
+hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, const void* A,
+                               const float* dt, void* A_cumsum_out, hipStream_t s) {
+  dim3 grid(d.max_chunks, (d.H + 3) / 4);
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_chunk_cumsum<bf16>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
+                       reinterpret_cast<bf16*>(A_cumsum_out));
+  else
+    hipLaunchKernelGGL(k_chunk_cumsum<float>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
+                       reinterpret_cast<float*>(A_cumsum_out));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// decay_chunk = exp(clamp(segsum(pad(A_cumsum[..., -1], (1, 0))))) in the
+// input dtype (ssd_scan.py:402-406): the segsum is accumulated in fp32 down
+// each column from j+1 (:104-116), rounded to the dtype, then exp-clamped and
+// rounded again, as the reference's two kernels do. One block per (b, h).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void k_decay_chunk(int nch, int Q, const T* __restrict__ Acs, T* __restrict__ out) {
+  const int bh = blockIdx.x;
+  const int n = nch + 1;
+  const T* a = Acs + (int64_t)bh * nch * Q;
+  T* o = out + (int64_t)bh * n * n;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    float acc = 0.0f;
+    for (int i = 0; i < n; ++i) {
+      float seg;
+      if (i < j) {
+        seg = -1e4f;
+      } else {
+        if (i > j) acc += to_f(a[(int64_t)(i - 1) * Q + (Q - 1)]);  // v_i = A_cumsum[i-1, Q-1]
+        seg = acc;
+      }
+      seg = to_f(from_f<T>(fminf(fmaxf(seg, SSD_LO), SSD_HI)));
+      o[(int64_t)i * n + j] = from_f<T>(__expf(fminf(fmaxf(seg, SSD_LO), SSD_HI)));
+    }
+  }
+}
+
+hipError_t launch_decay_chunk(int dtype, int batch, int H, int nch, int Q, const void* Acs, void* out,
+                              hipStream_t s) {
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_decay_chunk<bf16>, dim3(batch * H), dim3(256), 0, s, nch, Q,
+                       reinterpret_cast<const bf16*>(Acs), reinterpret_cast<bf16*>(out));
+  else
+    hipLaunchKernelGGL(k_decay_chunk<float>, dim3(batch * H), dim3(256), 0, s, nch, Q,
+                       reinterpret_cast<const float*>(Acs), reinterpret_cast<float*>(out));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// L = exp(clamp(segsum(a))) per (b, h, chunk), a permuted to (b, h, c, l)
+// (ssd_scan.py:380-382). Thread per column j, walking rows i: the same fp32
+// accumulation order as the reference segsum kernel (:104-116).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void k_materialize_L(int seqlen, int H, int Q, const T* __restrict__ a, T* __restrict__ L) {
+  const int nch = seqlen / Q;
+  const int k = blockIdx.x % nch;
+  const int h = (blockIdx.x / nch) % H;
+  const int b = blockIdx.x / (nch * H);
+  T* o = L + (int64_t)blockIdx.x * Q * Q;  // (b, h, c) major order matches blockIdx
+  for (int j = threadIdx.x; j < Q; j += blockDim.x) {
+    float acc = 0.0f;
+    for (int i = 0; i < Q; ++i) {
+      float seg;
+      if (i < j) {
+        seg = -1e4f;
+      } else {
+        if (i > j) acc += to_f(a[((int64_t)b * seqlen + (int64_t)k * Q + i) * H + h]);
+        seg = acc;
+      }
+      seg = to_f(from_f<T>(fminf(fmaxf(seg, SSD_LO), SSD_HI)));
+      o[(int64_t)i * Q + j] = from_f<T>(__expf(fminf(fmaxf(seg, SSD_LO), SSD_HI)));
+    }
+  }
+}
+
+hipError_t launch_materialize_L(int dtype, int batch, int seqlen, int H, int Q, const void* a, void* L,
+                                hipStream_t s) {
+  const int blocks = batch * H * (seqlen / Q);
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_materialize_L<bf16>, dim3(blocks), dim3(256), 0, s, seqlen, H, Q,
+                       reinterpret_cast<const bf16*>(a), reinterpret_cast<bf16*>(L));
+  else
+    hipLaunchKernelGGL(k_materialize_L<float>, dim3(blocks), dim3(256), 0, s, seqlen, H, Q,
+                       reinterpret_cast<const float*>(a), reinterpret_cast<float*>(L));
+  return hipGetLastError();
+}

@@ -1,0 +1,80 @@
+// Deterministic reductions of per-block partials (fixed summation order, no
+// atomics), so repeated backward calls are bitwise identical.
+#include "ssd_launch.h"
+
+// out[i] = sum_s part[s][i], s = 0..nslices-1 in order.
+template <typename T>
+__global__ void k_reduce_slices(int64_t nelem, int nslices, const float* __restrict__ part, T* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nelem; i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int s = 0; s < nslices; ++s) acc += part[(int64_t)s * nelem + i];
+    out[i] = from_f<T>(acc);
+  }
+}
+
+hipError_t launch_reduce_slices(int dtype, int64_t nelem, int nslices, const float* part, void* out,
+                                hipStream_t s) {
+  int64_t blocks64 = (nelem + 255) / 256;
+  if (blocks64 > 65536) blocks64 = 65536;
+  if (blocks64 < 1) blocks64 = 1;
+  const unsigned blocks = (unsigned)blocks64;
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_reduce_slices<bf16>, dim3(blocks), dim3(256), 0, s, nelem, nslices, part,
+                       reinterpret_cast<bf16*>(out));
+  else
+    hipLaunchKernelGGL(k_reduce_slices<float>, dim3(blocks), dim3(256), 0, s, nelem, nslices, part,
+                       reinterpret_cast<float*>(out));
+  return hipGetLastError();
+}
+
+// One block per head: dA[h] = sum over valid chunks of dA_part; dD[h] = sum
+// over valid (chunk, column block) of dD_part. Tree order fixed.
+__global__ void __launch_bounds__(256) k_reduce_heads(SsdDims d, const ChunkInfo* __restrict__ chunks,
+                                                      const float* __restrict__ dA_part,
+                                                      const float* __restrict__ dD_part, float* __restrict__ dA,
+                                                      float* __restrict__ dD) {
+  __shared__ float ra[256], rd[256];
+  const int h = blockIdx.x;
+  const int nrb = d.Qpad / SSD_BLK;
+  float a = 0.0f, dd = 0.0f;
+  for (int c = threadIdx.x; c < d.max_chunks; c += blockDim.x) {
+    const int len = chunks[c].len;
+    if (len == 0) continue;
+    a += dA_part[(int64_t)c * d.H + h];
+    for (int j = 0; j < nrb; ++j)
+      if (j * SSD_BLK < len) dd += dD_part[((int64_t)c * d.H + h) * nrb + j];
+  }
+  ra[threadIdx.x] = a;
+  rd[threadIdx.x] = dd;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      ra[threadIdx.x] += ra[threadIdx.x + o];
+      rd[threadIdx.x] += rd[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (dA) dA[h] = ra[0];
+    if (dD) dD[h] = rd[0];
+  }
+}
+
+hipError_t launch_reduce_heads(const SsdDims& d, const SsdBufs& b, float* dA_head, float* dD, hipStream_t s) {
+  hipLaunchKernelGGL(k_reduce_heads, dim3(d.H), dim3(256), 0, s, d, b.chunks, b.dA_part, b.dD_part, dA_head, dD);
+  return hipGetLastError();
+}
+
+// out[k] = sum_b part[b][k], b in order.
+__global__ void k_reduce_rows(int nblocks, int width, const float* __restrict__ part, float* __restrict__ out) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= width) return;
+  float acc = 0.0f;
+  for (int b = 0; b < nblocks; ++b) acc += part[(int64_t)b * width + k];
+  out[k] = acc;
+}
+
+hipError_t launch_reduce_rows(int nblocks, int width, const float* part, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_reduce_rows, dim3((width + 255) / 256), dim3(256), 0, s, nblocks, width, part, out);
+  return hipGetLastError();
+}

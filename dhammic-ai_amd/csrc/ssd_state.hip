@@ -1,0 +1,238 @@
+// Chunk-local states on MFMA and the inter-chunk state recurrence.
+#include "ssd_launch.h"
+
+// ---------------------------------------------------------------------------
+// out[c][h][p][n] = sum_{l < len} U[row0+l][h][p] * coef_l * V[row0+l][g][n]
+//   mode 0 (forward chunk states, ssd_scan.py:387-392):
+//       U = x, V = B, coef_l = exp(clamp(cs_last - cs_l)) * dt_l
+//   mode 1 (backward, gradient of the entering state from Y_off, :412-415):
+//       U = dy, V = C, coef_l = exp(clamp(cs_l))
+// One block per (chunk, head): a (Ppad x Npad) fp32 tile, K = tokens of the
+// chunk in slabs of 64. U and V are staged transposed (token index
+// contiguous) so both MFMA operands are k-contiguous.
+// ---------------------------------------------------------------------------
+template <typename T, int MODE>
+__global__ void __launch_bounds__(256) k_chunk_state(SsdDims d, const ChunkInfo* __restrict__ chunks,
+                                                     const float* __restrict__ cs, const T* __restrict__ U,
+                                                     const T* __restrict__ V, const float* __restrict__ dt,
+                                                     float* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int c = blockIdx.x, h = blockIdx.y;
+  const ChunkInfo ci = chunks[c];
+  if (ci.len == 0) return;
+  const int g = h / d.hpg;
+  const int KP = lds_pitch<T>(SSD_BLK);
+  T* UT = reinterpret_cast<T*>(smem);                 // [Ppad][KP]
+  T* VT = UT + d.Ppad * KP;                            // [Npad][KP]
+  float* coef = reinterpret_cast<float*>(VT + d.Npad * KP);  // [Qpad]
+  const float* csc = cs + ((int64_t)c * d.H + h) * d.Qpad;
+  const float cs_last = csc[d.Qpad - 1];
+  for (int l = threadIdx.x; l < d.Qpad; l += blockDim.x) {
+    float v = 0.0f;
+    if (l < ci.len) {
+      if (MODE == 0) {
+        v = exp_clamp(cs_last - csc[l]) * (d.has_dt ? dt[(int64_t)(ci.row0 + l) * d.H + h] : 1.0f);
+      } else {
+        v = exp_clamp(csc[l]);
+      }
+    }
+    coef[l] = v;
+  }
+  const int w = threadIdx.x >> 6, wr = w & 1, wc = w >> 1;
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) zero(acc[a][b]);
+  const int64_t urow = (int64_t)d.H * d.P, vrow = (int64_t)d.G * d.N;
+  for (int kb = 0; kb < ci.len; kb += SSD_BLK) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < SSD_BLK * d.Ppad; idx += blockDim.x) {
+      const int l = idx / d.Ppad, p = idx % d.Ppad;
+      float v = 0.0f;
+      if (kb + l < ci.len && p < d.P) v = to_f(U[(int64_t)(ci.row0 + kb + l) * urow + (int64_t)h * d.P + p]);
+      UT[p * KP + l] = from_f<T>(v);
+    }
+    for (int idx = threadIdx.x; idx < SSD_BLK * d.Npad; idx += blockDim.x) {
+      const int l = idx / d.Npad, n = idx % d.Npad;
+      float v = 0.0f;
+      if (kb + l < ci.len && n < d.N)
+        v = coef[kb + l] * to_f(V[(int64_t)(ci.row0 + kb + l) * vrow + (int64_t)g * d.N + n]);
+      VT[n * KP + l] = from_f<T>(v);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+      const int p0 = wr * 32 + 64 * tp;
+      if (p0 >= d.Ppad) continue;
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn) {
+        const int n0 = wc * 32 + 64 * tn;
+        if (n0 >= d.Npad) continue;
+        mma_tile<T>(acc[tp][tn], UT + p0 * KP, KP, VT + n0 * KP, KP, SSD_BLK);
+      }
+    }
+  }
+  const int lane = lane_id();
+  float* o = out + ((int64_t)c * d.H + h) * d.Ppad * d.Npad;
+#pragma unroll
+  for (int tp = 0; tp < 2; ++tp) {
+    const int p0 = wr * 32 + 64 * tp;
+    if (p0 >= d.Ppad) continue;
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      const int n0 = wc * 32 + 64 * tn;
+      if (n0 >= d.Npad) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        o[(int64_t)(p0 + acc_row(v, lane)) * d.Npad + n0 + (lane & 31)] = acc[tp][tn][v];
+    }
+  }
+}
+
+static size_t lds_chunk_state(int dtype, const SsdDims& d) {
+  const size_t es = dtype == 1 ? 2 : 4;
+  const int KP = SSD_BLK + 16 / (int)es;
+  return es * (size_t)(d.Ppad + d.Npad) * KP + sizeof(float) * d.Qpad;
+}
+
+hipError_t launch_chunk_state(int dtype, int mode, const SsdDims& d, const SsdBufs& b, const void* U,
+                              const void* V, const float* dt, float* out, hipStream_t s) {
+  dim3 grid(d.max_chunks, d.H);
+  const size_t lds = lds_chunk_state(dtype, d);
+  if (dtype == 1) {
+    auto k = mode == 0 ? k_chunk_state<bf16, 0> : k_chunk_state<bf16, 1>;
+    ensure_lds(k, lds);
+    hipLaunchKernelGGL(k, grid, dim3(256), lds, s, d, b.chunks, b.cs, reinterpret_cast<const bf16*>(U),
+                       reinterpret_cast<const bf16*>(V), dt, out);
+  } else {
+    auto k = mode == 0 ? k_chunk_state<float, 0> : k_chunk_state<float, 1>;
+    ensure_lds(k, lds);
+    hipLaunchKernelGGL(k, grid, dim3(256), lds, s, d, b.chunks, b.cs, reinterpret_cast<const float*>(U),
+                       reinterpret_cast<const float*>(V), dt, out);
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Forward recurrence over the chunks of one sequence (ssd_scan.py:394-410):
+//   hin[c] = run;  run = exp(clamp(total_c)) * run + st[c];  final = run
+// starting from the sequence's initial state (or 0). Thread per (p, n)
+// element; fp32 state in registers. The reference forms the same recurrence
+// as a (c+1)x(c+1) matrix with the clamp applied to multi-chunk sums; the two
+// differ only where a product of decays falls below e^-20.
+// ---------------------------------------------------------------------------
+template <typename T, typename S>
+__global__ void __launch_bounds__(SSD_PASS_THREADS) k_state_pass_fwd(SsdDims d, const int32_t* __restrict__ seq_chunk0,
+                                                                     const float* __restrict__ cs,
+                                                                     const float* __restrict__ st, T* __restrict__ hin,
+                                                                     const S* __restrict__ init, S* __restrict__ fin) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  const int h = blockIdx.y, sq = blockIdx.z;
+  const int PN = d.Ppad * d.Npad;
+  if (e >= PN) return;
+  const int p = e / d.Npad, n = e % d.Npad;
+  const bool real = p < d.P && n < d.N;
+  const int64_t sidx = (((int64_t)sq * d.H + h) * d.P + p) * d.N + n;
+  float run = (init && real) ? to_f(init[sidx]) : 0.0f;
+  const int c0 = seq_chunk0[sq], c1 = seq_chunk0[sq + 1];
+  for (int c = c0; c < c1; ++c) {
+    const int64_t off = ((int64_t)c * d.H + h) * PN + e;
+    const float s_c = st[off];
+    const float tot = cs[((int64_t)c * d.H + h) * d.Qpad + d.Qpad - 1];
+    hin[off] = from_f<T>(run);
+    run = exp_clamp(tot) * run + s_c;
+  }
+  if (fin && real) fin[sidx] = from_f<S>(run);
+}
+
+// ---------------------------------------------------------------------------
+// Reverse recurrence: gradient of the state leaving chunk c is
+//   dst[c] = run;  run = exp(clamp(total_c)) * run + dh_local[c]
+// from dfinal (or 0); dinit = run at the start. Also the gradient of each
+// chunk total, sum_{p,n} dst[c] * exp(total_c) * hin[c] (strict clamp mask),
+// reduced per block into dtot_part (deterministic order).
+// ---------------------------------------------------------------------------
+template <typename T, typename S>
+__global__ void __launch_bounds__(SSD_PASS_THREADS) k_state_pass_bwd(SsdDims d, const int32_t* __restrict__ seq_chunk0,
+                                                                     const float* __restrict__ cs, float* __restrict__ buf,
+                                                                     const T* __restrict__ hin, const S* __restrict__ dfin,
+                                                                     S* __restrict__ dinit, float* __restrict__ dtot_part) {
+  __shared__ float red[SSD_PASS_THREADS / 64];
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  const int h = blockIdx.y, sq = blockIdx.z;
+  const int PN = d.Ppad * d.Npad;
+  const bool inside = e < PN;
+  const int p = inside ? e / d.Npad : 0, n = inside ? e % d.Npad : 0;
+  const bool real = inside && p < d.P && n < d.N;
+  const int64_t sidx = (((int64_t)sq * d.H + h) * d.P + p) * d.N + n;
+  float run = (dfin && real) ? to_f(dfin[sidx]) : 0.0f;
+  const int c0 = seq_chunk0[sq], c1 = seq_chunk0[sq + 1];
+  const int nblk = gridDim.x;
+  for (int c = c1 - 1; c >= c0; --c) {
+    const int64_t off = ((int64_t)c * d.H + h) * PN + e;
+    const float tot = cs[((int64_t)c * d.H + h) * d.Qpad + d.Qpad - 1];
+    const float dec = exp_clamp(tot);
+    float contrib = 0.0f;
+    float dhl = 0.0f;
+    if (inside) {
+      dhl = buf[off];
+      buf[off] = run;
+      contrib = run * dec * to_f(hin[off]) * clamp_pass(tot);
+    }
+    // block reduction of contrib (wave shuffle, then the 4 wave sums in order)
+    for (int o = 32; o > 0; o >>= 1) contrib += __shfl_xor(contrib, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = contrib;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float sum = 0.0f;
+      for (int w = 0; w < SSD_PASS_THREADS / 64; ++w) sum += red[w];
+      dtot_part[((int64_t)c * d.H + h) * nblk + blockIdx.x] = sum;
+    }
+    __syncthreads();
+    run = dec * run + dhl;
+  }
+  if (dinit && real) dinit[sidx] = from_f<S>(run);
+}
+
+template <typename T>
+static hipError_t pass_fwd_t(int state_dtype, const SsdDims& d, const SsdBufs& b, const void* init,
+                             void* fin, hipStream_t s) {
+  dim3 grid(b.npass_blk, d.H, d.nseq);
+  if (state_dtype == 1)
+    hipLaunchKernelGGL((k_state_pass_fwd<T, bf16>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
+                       b.st, reinterpret_cast<T*>(b.hin), reinterpret_cast<const bf16*>(init),
+                       reinterpret_cast<bf16*>(fin));
+  else
+    hipLaunchKernelGGL((k_state_pass_fwd<T, float>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
+                       b.st, reinterpret_cast<T*>(b.hin), reinterpret_cast<const float*>(init),
+                       reinterpret_cast<float*>(fin));
+  return hipGetLastError();
+}
+
+hipError_t launch_state_pass_fwd(int dtype, int state_dtype, const SsdDims& d, const SsdBufs& b,
+                                 const void* init, void* final_state, hipStream_t s) {
+  return dtype == 1 ? pass_fwd_t<bf16>(state_dtype, d, b, init, final_state, s)
+                    : pass_fwd_t<float>(state_dtype, d, b, init, final_state, s);
+}
+
+template <typename T>
+static hipError_t pass_bwd_t(int state_dtype, const SsdDims& d, const SsdBufs& b, const void* dfin,
+                             void* dinit, hipStream_t s) {
+  dim3 grid(b.npass_blk, d.H, d.nseq);
+  if (state_dtype == 1)
+    hipLaunchKernelGGL((k_state_pass_bwd<T, bf16>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
+                       b.dst, reinterpret_cast<const T*>(b.hin), reinterpret_cast<const bf16*>(dfin),
+                       reinterpret_cast<bf16*>(dinit), b.dtot_part);
+  else
+    hipLaunchKernelGGL((k_state_pass_bwd<T, float>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
+                       b.dst, reinterpret_cast<const T*>(b.hin), reinterpret_cast<const float*>(dfin),
+                       reinterpret_cast<float*>(dinit), b.dtot_part);
+  return hipGetLastError();
+}
+
+hipError_t launch_state_pass_bwd(int dtype, int state_dtype, const SsdDims& d, const SsdBufs& b,
+                                 const void* dfinal, void* dinit, hipStream_t s) {
+  return dtype == 1 ? pass_bwd_t<bf16>(state_dtype, d, b, dfinal, dinit, s)
+                    : pass_bwd_t<float>(state_dtype, d, b, dfinal, dinit, s);
+}

@@ -1,0 +1,121 @@
+"""ctypes binding of include/ssd_mi355x.h (libssd_mi355x.so).
+
+torch is imported before the library is opened so that the library's
+libamdhip64.so.7 dependency resolves to the HIP runtime torch already loaded
+(one runtime per process: torch's streams and allocations are valid in it).
+There is no fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL, see above)
+
+LIB_PATH = Path(__file__).resolve().with_name("libssd_mi355x.so")
+
+SSD_OK = 0
+SSD_ERR_INVALID = -1
+SSD_ERR_UNSUPPORTED = -2
+SSD_ERR_WORKSPACE = -3
+SSD_ERR_HIP = -4
+
+SSD_DTYPE_F32 = 0
+SSD_DTYPE_BF16 = 1
+
+SSD_A_PER_HEAD = 0
+SSD_A_PER_TOKEN = 1
+SSD_A_CUMSUM = 2
+
+# enum ssd_phase (launch order of ssd_fwd / ssd_bwd)
+PHASES = ("chunk_table", "cumsum", "fwd_state", "fwd_pass", "fwd_scan", "norm_fwd", "norm_bwd", "norm_dw",
+          "bwd_state", "bwd_pass", "bwd_col", "bwd_row", "bwd_finish", "bwd_reduce_bc", "bwd_reduce_heads")
+SSD_NUM_PHASES = len(PHASES)
+
+SSD_WS_SAVED = 0
+SSD_WS_FWD_SCRATCH = 1
+SSD_WS_BWD_SCRATCH = 2
+
+ABI_VERSION = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_vp = ctypes.c_void_p
+
+
+class SsdDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("seqlen", _i64), ("nheads", _i64), ("headdim", _i64),
+        ("ngroups", _i64), ("dstate", _i64), ("chunk", _i64), ("nseq", _i64),
+        ("dtype", _i32), ("state_dtype", _i32), ("a_mode", _i32),
+        ("has_dt", _i32), ("has_D", _i32), ("has_z", _i32), ("has_init", _i32),
+        ("has_dfinal", _i32), ("varlen", _i32), ("want_final", _i32), ("want_A_cumsum", _i32),
+        ("norm_eps", ctypes.c_float),
+    ]
+
+
+_IN_FIELDS = [("x", _vp), ("dt", _vp), ("A", _vp), ("B", _vp), ("C", _vp), ("D", _vp),
+              ("z", _vp), ("norm_weight", _vp), ("init", _vp), ("cu_seqlens", _vp)]
+
+
+class SsdFwdArgs(ctypes.Structure):
+    _fields_ = _IN_FIELDS + [("y", _vp), ("final_state", _vp), ("A_cumsum_out", _vp), ("events", _vp)]
+
+
+class SsdBwdArgs(ctypes.Structure):
+    _fields_ = _IN_FIELDS + [
+        ("dy", _vp), ("dfinal", _vp),
+        ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp), ("dC", _vp), ("dD", _vp),
+        ("dz", _vp), ("dnorm_weight", _vp), ("dinit", _vp), ("events", _vp),
+    ]
+
+
+# Every symbol include/ssd_mi355x.h declares.
+EXPORTS = ("ssd_validate", "ssd_workspace_bytes", "ssd_fwd", "ssd_bwd", "ssd_materialize_L",
+           "ssd_decay_chunk", "ssd_status_string", "ssd_abi_version")
+
+_lib = None
+
+
+def load():
+    """Open the library once and declare the prototypes."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python dhammic-ai_amd/build.py` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    P = ctypes.POINTER
+    lib.ssd_validate.argtypes = [P(SsdDesc)]
+    lib.ssd_validate.restype = ctypes.c_int
+    lib.ssd_workspace_bytes.argtypes = [P(SsdDesc), ctypes.c_int]
+    lib.ssd_workspace_bytes.restype = ctypes.c_size_t
+    lib.ssd_fwd.argtypes = [P(SsdDesc), P(SsdFwdArgs), _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]
+    lib.ssd_fwd.restype = ctypes.c_int
+    lib.ssd_bwd.argtypes = [P(SsdDesc), P(SsdBwdArgs), _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]
+    lib.ssd_bwd.restype = ctypes.c_int
+    lib.ssd_materialize_L.argtypes = [P(SsdDesc), _vp, _vp, _vp]
+    lib.ssd_materialize_L.restype = ctypes.c_int
+    lib.ssd_decay_chunk.argtypes = [P(SsdDesc), _vp, _vp, _vp]
+    lib.ssd_decay_chunk.restype = ctypes.c_int
+    lib.ssd_status_string.argtypes = [ctypes.c_int]
+    lib.ssd_status_string.restype = ctypes.c_char_p
+    lib.ssd_abi_version.argtypes = []
+    lib.ssd_abi_version.restype = ctypes.c_int
+    if lib.ssd_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH}: ABI {lib.ssd_abi_version()} != {ABI_VERSION}; rebuild")
+    _lib = lib
+    return lib
+
+
+def check(status: int, what: str):
+    """Map a status code to the exception a caller of the reference op would see."""
+    if status == SSD_OK:
+        return
+    msg = f"{what}: {load().ssd_status_string(status).decode()} (status {status})"
+    if status == SSD_ERR_INVALID:
+        raise ValueError(msg)
+    if status == SSD_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,378 @@
+"""Fused chunked SSD scan on MI355X: the reference's Python API over the HIP C ABI.
+
+Drop-in for r2/dhammic-ai/src/kernels/ssd_scan.py:
+  * ``fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None)``
+    -> ``(Y, final_state, cache)``                                  (:539-583)
+  * ``FusedSSDScan.apply(x, A, B, C, chunk_size, initial_states, L, decay_chunk,
+    A_cumsum)`` -> ``(Y, final_state, L, decay_chunk, A_cumsum)``; backward
+    returns the nine slots of :533                                  (:427-533)
+plus the extended entry ``ssd_scan_combined`` (dt, per-head A, grouped B/C,
+D, gated RMSNorm, initial/final states, packed varlen via cu_seqlens) that
+the caller composes around the op (r2/dhammic-ai/src/mamba_base_engine.py:
+152-191).
+
+All device work runs in libssd_mi355x.so (gfx950 HIP kernels) on the current
+torch stream; torch only allocates the tensors and the workspaces. There is
+no CPU or eager fallback: a CPU tensor or a missing library raises.
+
+Reference behaviour kept: same signatures, shapes, dtypes and return
+conventions; ``T % chunk_size == 0`` raises AssertionError; with a cache the
+decay comes from ``cache["A_cumsum"]`` and A gets no gradient (:364-406,
+:533). Differences (all below the parity tolerance): the acausal e^-20
+entries of the reference's clamped -1e4 fill are exact zeros here, the
+inter-chunk recurrence clamps each chunk's decay instead of multi-chunk
+sums, and decays are computed in fp32 from an fp32 cumsum whatever the input
+dtype. The returned cache's ``L`` and ``decay_chunk`` are materialised on
+first access (they are never needed by the kernels).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _capi as C_
+
+__all__ = ["fused_ssd_scan", "FusedSSDScan", "ssd_scan_combined"]
+
+_DTYPES = {torch.float32: C_.SSD_DTYPE_F32, torch.bfloat16: C_.SSD_DTYPE_BF16}
+
+
+def _code(dtype, what):
+    if dtype not in _DTYPES:
+        raise TypeError(f"{what}: dtype {dtype} is not supported (bfloat16 or float32)")
+    return _DTYPES[dtype]
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+@dataclass(frozen=True)
+class _Cfg:
+    chunk: int
+    a_mode: int
+    nseq: int
+    varlen: bool
+    state_code: int
+    want_acs: bool
+    eps: float
+
+
+def _desc(cfg: _Cfg, x, B, dt, D, z, init, has_dfinal=False):
+    b, T, H, P = x.shape
+    d = C_.SsdDesc()
+    d.batch, d.seqlen, d.nheads, d.headdim = b, T, H, P
+    d.ngroups, d.dstate, d.chunk, d.nseq = B.shape[2], B.shape[3], cfg.chunk, cfg.nseq
+    d.dtype = _code(x.dtype, "x")
+    d.state_dtype = cfg.state_code
+    d.a_mode = cfg.a_mode
+    d.has_dt = int(dt is not None)
+    d.has_D = int(D is not None)
+    d.has_z = int(z is not None)
+    d.has_init = int(init is not None)
+    d.has_dfinal = int(has_dfinal)
+    d.varlen = int(cfg.varlen)
+    d.want_final = 1
+    d.want_A_cumsum = int(cfg.want_acs)
+    d.norm_eps = cfg.eps
+    return d
+
+
+def _check_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise AssertionError("fused SSD scan: all tensors must be on the GPU (got a CPU tensor)")
+
+
+def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu):
+    """Run ssd_fwd. Returns (y, final_state, A_cumsum_out or empty, saved workspace)."""
+    lib = C_.load()
+    _check_device(x, dt, A, B, C, D, z, w, init, cu)
+    desc = _desc(cfg, x, B, dt, D, z, init)
+    C_.check(lib.ssd_validate(ctypes.byref(desc)), "ssd_fwd")
+    b, T, H, P = x.shape
+    N = B.shape[3]
+    dev = x.device
+    y = torch.empty_like(x)
+    sdt = torch.float32 if cfg.state_code == C_.SSD_DTYPE_F32 else torch.bfloat16
+    final = torch.empty((cfg.nseq, H, P, N), dtype=sdt, device=dev)
+    acs = (torch.empty((b, H, T // cfg.chunk, cfg.chunk), dtype=x.dtype, device=dev)
+           if cfg.want_acs else x.new_empty(0))
+    saved = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_SAVED), dtype=torch.uint8,
+                        device=dev)
+    scratch = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_FWD_SCRATCH),
+                          dtype=torch.uint8, device=dev)
+    args = C_.SsdFwdArgs(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(w), _p(init), _p(cu),
+                         _p(y), _p(final), _p(acs) if cfg.want_acs else None)
+    with torch.cuda.device(dev):
+        st = lib.ssd_fwd(ctypes.byref(desc), ctypes.byref(args), _p(saved), saved.numel(), _p(scratch),
+                         scratch.numel(), _stream(dev))
+    C_.check(st, "ssd_fwd")
+    return y, final, acs, saved
+
+
+def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal):
+    """Run ssd_bwd. Returns dict of gradients (None where the input is absent)."""
+    lib = C_.load()
+    desc = _desc(cfg, x, B, dt, D, z, init, has_dfinal=dfinal is not None)
+    dev = x.device
+    dy = torch.zeros_like(x) if dy is None else dy.contiguous()
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    if dfinal is not None:
+        sdt = torch.float32 if cfg.state_code == C_.SSD_DTYPE_F32 else torch.bfloat16
+        dfinal = dfinal.to(sdt).contiguous()
+    g = {
+        "x": torch.empty_like(x), "B": torch.empty_like(B), "C": torch.empty_like(C),
+        "dt": torch.empty_like(dt) if dt is not None else None,
+        "A": (torch.empty_like(A) if cfg.a_mode in (C_.SSD_A_PER_HEAD, C_.SSD_A_PER_TOKEN) else None),
+        "D": torch.empty_like(D) if D is not None else None,
+        "z": torch.empty_like(z) if z is not None else None,
+        "w": torch.empty_like(w) if (w is not None and z is not None) else None,
+        "init": torch.empty_like(init) if init is not None else None,
+    }
+    scratch = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_BWD_SCRATCH),
+                          dtype=torch.uint8, device=dev)
+    args = C_.SsdBwdArgs(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(w), _p(init), _p(cu),
+                         _p(dy), _p(dfinal),
+                         _p(g["x"]), _p(g["dt"]), _p(g["A"]), _p(g["B"]), _p(g["C"]), _p(g["D"]),
+                         _p(g["z"]), _p(g["w"]), _p(g["init"]))
+    with torch.cuda.device(dev):
+        st = lib.ssd_bwd(ctypes.byref(desc), ctypes.byref(args), _p(saved_ws), saved_ws.numel(), _p(scratch),
+                         scratch.numel(), _stream(dev))
+    C_.check(st, "ssd_bwd")
+    return g
+
+
+class _SsdFunction(torch.autograd.Function):
+    """Autograd node over ssd_fwd / ssd_bwd (inputs already contiguous)."""
+
+    @staticmethod
+    def forward(ctx, cfg, x, dt, A, B, C, D, z, w, init, cu):
+        ctx.set_materialize_grads(False)
+        y, final, acs, saved = _forward(cfg, x, dt, A, B, C, D, z, w, init, cu)
+        ctx.cfg = cfg
+        ctx.ws = saved
+        ctx.save_for_backward(x, dt, A, B, C, D, z, w, init, cu)
+        ctx.mark_non_differentiable(acs)
+        return y, final, acs
+
+    @staticmethod
+    def backward(ctx, dy, dfinal, _dacs):
+        x, dt, A, B, C, D, z, w, init, cu = ctx.saved_tensors
+        if dy is None and dfinal is None:
+            return (None,) * 11
+        g = _backward(ctx.cfg, ctx.ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal)
+        ni = ctx.needs_input_grad
+        pick = lambda k, i: g[k] if ni[i] else None  # noqa: E731
+        return (None, pick("x", 1), pick("dt", 2), pick("A", 3), pick("B", 4), pick("C", 5),
+                pick("D", 6), pick("z", 7), pick("w", 8), pick("init", 9), None)
+
+
+# --------------------------------------------------------------------------- #
+# Reference cache (L, decay_chunk, A_cumsum)
+# --------------------------------------------------------------------------- #
+def _cache_desc(a_like, chunk):
+    b, T, H = a_like.shape[:3]
+    d = C_.SsdDesc()
+    d.batch, d.seqlen, d.nheads, d.headdim, d.ngroups, d.dstate, d.chunk = b, T, H, 1, 1, 1, chunk
+    d.dtype = _code(a_like.dtype, "A")
+    return d
+
+
+class _LazyCache(dict):
+    """The reference's cache dict {L, decay_chunk, A_cumsum}
+    (ssd_scan.py:420, shapes pinned by tests/kernels/test_ssd_scan.py:104-110).
+    ``A_cumsum`` is filled by the forward; ``L`` and ``decay_chunk`` are
+    computed on first access from the per-token log-decay and A_cumsum."""
+
+    def __init__(self, a, A_cumsum, chunk):
+        super().__init__(L=None, decay_chunk=None, A_cumsum=A_cumsum)
+        self._a = a
+        self._chunk = chunk
+
+    def _fill(self, key):
+        v = dict.__getitem__(self, key)
+        if v is None and key in ("L", "decay_chunk"):
+            lib = C_.load()
+            acs = dict.__getitem__(self, "A_cumsum")
+            b, H, nch, Q = acs.shape
+            desc = _cache_desc(self._a, self._chunk)
+            dev = acs.device
+            with torch.cuda.device(dev):
+                if key == "L":
+                    v = torch.empty((b, H, nch, Q, Q), dtype=acs.dtype, device=dev)
+                    C_.check(lib.ssd_materialize_L(ctypes.byref(desc), _p(self._a), _p(v), _stream(dev)),
+                             "ssd_materialize_L")
+                else:
+                    v = torch.empty((b, H, nch + 1, nch + 1), dtype=acs.dtype, device=dev)
+                    C_.check(lib.ssd_decay_chunk(ctypes.byref(desc), _p(acs), _p(v), _stream(dev)),
+                             "ssd_decay_chunk")
+            dict.__setitem__(self, key, v)
+        return v
+
+    def __getitem__(self, key):
+        return self._fill(key)
+
+    def get(self, key, default=None):
+        return self._fill(key) if key in self else default
+
+    def __iter__(self):
+        return iter(list(dict.keys(self)))
+
+    def values(self):
+        return [self._fill(k) for k in self]
+
+    def items(self):
+        return [(k, self._fill(k)) for k in self]
+
+    def copy(self):
+        c = _LazyCache(self._a, dict.__getitem__(self, "A_cumsum"), self._chunk)
+        for k in ("L", "decay_chunk"):
+            dict.__setitem__(c, k, dict.__getitem__(self, k))
+        return c
+
+    def cumsum_tensor(self):
+        return dict.__getitem__(self, "A_cumsum")
+
+
+def _reference_cfg(x, chunk, a_mode, want_acs):
+    return _Cfg(chunk=chunk, a_mode=a_mode, nseq=x.shape[0], varlen=False,
+                state_code=_code(x.dtype, "x"), want_acs=want_acs, eps=0.0)
+
+
+def _check_reference_inputs(x, A, B, C, chunk_size):
+    assert x.shape[1] % chunk_size == 0, (
+        f"sequence length {x.shape[1]} not divisible by chunk_size {chunk_size}")
+    _check_device(x, A, B, C)
+    if not (x.dtype == A.dtype == B.dtype == C.dtype):
+        raise RuntimeError(f"fused_ssd_scan: x, A, B, C must share one dtype "
+                           f"(got {x.dtype}, {A.dtype}, {B.dtype}, {C.dtype})")
+
+
+def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
+    """Fused SSD chunked-parallel scan (ssd_scan.py:539-583).
+
+    Args:
+        x: (b, seqlen, n_heads, d_head), bf16 or fp32, on the GPU.
+        A: (b, seqlen, n_heads) per-token log-decay, same dtype.
+        B, C: (b, seqlen, n_heads, d_state), same dtype.
+        chunk_size: seqlen must be divisible by this (AssertionError otherwise).
+        initial_states: optional (b, 1, n_heads, d_head, d_state); zeros if None.
+        cache: optional dict from a prior call; its A_cumsum replaces A, and A
+            then receives no gradient (as in the reference).
+
+    Returns:
+        Y (b, seqlen, n_heads, d_head), final_state (b, n_heads, d_head, d_state),
+        cache {L, decay_chunk, A_cumsum}.
+    """
+    chunk = int(chunk_size)
+    _check_reference_inputs(x, A, B, C, chunk)
+    b, T, H, P = x.shape
+    N = B.shape[-1]
+    init = None if initial_states is None else initial_states.reshape(b, H, P, N).contiguous()
+    if cache is not None:
+        acs = cache.cumsum_tensor() if isinstance(cache, _LazyCache) else cache.get("A_cumsum")
+        if acs is None:
+            raise NotImplementedError("fused_ssd_scan: a cache without A_cumsum is not supported")
+        cfg = _reference_cfg(x, chunk, C_.SSD_A_CUMSUM, False)
+        Y, final, _ = _SsdFunction.apply(cfg, x.contiguous(), None, acs.detach().contiguous(), B.contiguous(),
+                                         C.contiguous(), None, None, None, init, None)
+        out = cache.copy() if isinstance(cache, _LazyCache) else {
+            "L": cache.get("L"), "decay_chunk": cache.get("decay_chunk"), "A_cumsum": acs}
+        return Y, final, out
+    cfg = _reference_cfg(x, chunk, C_.SSD_A_PER_TOKEN, True)
+    a = A.contiguous()
+    Y, final, acs = _SsdFunction.apply(cfg, x.contiguous(), None, a, B.contiguous(), C.contiguous(), None, None,
+                                       None, init, None)
+    return Y, final, _LazyCache(a.detach(), acs, chunk)
+
+
+class FusedSSDScan(torch.autograd.Function):
+    """The reference's autograd op with its exact 9-in / 5-out contract
+    (ssd_scan.py:427-533). L and decay_chunk are returned as tensors (the
+    cached ones when given). With A_cumsum supplied the decay comes from it
+    and dA is None; L / decay_chunk caches without A_cumsum are recomputed
+    from A (the kernels never read L)."""
+
+    @staticmethod
+    def forward(ctx, x, A, B, C, chunk_size, initial_states, L_cache_in, decay_chunk_cache_in,
+                A_cumsum_cache_in):
+        chunk = int(chunk_size)
+        _check_reference_inputs(x, A, B, C, chunk)
+        b, T, H, P = x.shape
+        N = B.shape[-1]
+        init = None if initial_states is None else initial_states.reshape(b, H, P, N).contiguous()
+        x, B, C = x.contiguous(), B.contiguous(), C.contiguous()
+        if A_cumsum_cache_in is not None:
+            cfg = _reference_cfg(x, chunk, C_.SSD_A_CUMSUM, False)
+            a_arg = A_cumsum_cache_in.detach().contiguous()
+        else:
+            cfg = _reference_cfg(x, chunk, C_.SSD_A_PER_TOKEN, True)
+            a_arg = A.detach().contiguous()
+        Y, final, acs, saved = _forward(cfg, x, None, a_arg, B, C, None, None, None, init, None)
+        if A_cumsum_cache_in is not None:
+            acs = A_cumsum_cache_in
+        lazy = _LazyCache(A.detach().contiguous(), acs, chunk)
+        L = L_cache_in if L_cache_in is not None else lazy["L"]
+        dc = decay_chunk_cache_in if decay_chunk_cache_in is not None else lazy["decay_chunk"]
+        ctx.cfg = cfg
+        ctx.ws = saved
+        ctx.has_init = initial_states is not None
+        ctx.init_shape = None if initial_states is None else initial_states.shape
+        ctx.save_for_backward(x, a_arg, B, C, init)
+        ctx.set_materialize_grads(False)
+        return Y, final, L, dc, acs
+
+    @staticmethod
+    def backward(ctx, dY, dfinal_state, dL_unused, ddecay_chunk_unused, dA_cumsum_unused):
+        x, a_arg, B, C, init = ctx.saved_tensors
+        if dY is None and dfinal_state is None:
+            return (None,) * 9
+        g = _backward(ctx.cfg, ctx.ws, x, None, a_arg, B, C, None, None, None, init, None, dY, dfinal_state)
+        ni = ctx.needs_input_grad
+        dA = g["A"] if (ni[1] and ctx.cfg.a_mode == C_.SSD_A_PER_TOKEN) else None
+        dinit = g["init"].reshape(ctx.init_shape) if (ctx.has_init and ni[5]) else None
+        return (g["x"] if ni[0] else None, dA, g["B"] if ni[2] else None, g["C"] if ni[3] else None,
+                None, dinit, None, None, None)
+
+
+def ssd_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, norm_weight=None, norm_eps=1e-6,
+                      initial_states=None, cu_seqlens=None, return_final_state=False):
+    """Extended SSD: Y = SSD(x*dt, dt*A, B, C) + D*x, then optionally
+    rmsnorm(Y over heads*headdim) * norm_weight * silu(z).
+
+    x (b, L, H, P) bf16/fp32; dt (b, L, H) positive; A (H,); B, C (b, L, G, N)
+    with head h reading group h // (H/G); D (H,); z like x; norm_weight (H*P,);
+    initial_states (nseq, H, P, N) fp32; cu_seqlens (nseq+1,) int32 offsets of
+    packed sequences (b must be 1; cu_seqlens[0] = 0, cu_seqlens[-1] = L).
+    Sequences need not be chunk multiples: each ends in a partial chunk.
+    Returns out (and final_states (nseq, H, P, N) fp32 when asked).
+    """
+    b, L, H, P = x.shape
+    _check_device(x, dt, A, B, C, D, z, norm_weight, initial_states)
+    if B.dtype != x.dtype or C.dtype != x.dtype or (z is not None and z.dtype != x.dtype):
+        raise RuntimeError("ssd_scan_combined: B, C and z must have x's dtype")
+    f32 = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
+    cu = None
+    nseq = b
+    if cu_seqlens is not None:
+        if b != 1:
+            raise ValueError("ssd_scan_combined: cu_seqlens needs batch == 1")
+        cu = cu_seqlens.to(device=x.device, dtype=torch.int32).contiguous()
+        nseq = cu.numel() - 1
+    if z is not None and norm_weight is None:
+        norm_weight = torch.ones(H * P, dtype=torch.float32, device=x.device)
+    cfg = _Cfg(chunk=int(chunk_size), a_mode=C_.SSD_A_PER_HEAD, nseq=nseq, varlen=cu is not None,
+               state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=float(norm_eps))
+    init = f32(initial_states)
+    out, final, _ = _SsdFunction.apply(cfg, x.contiguous(), f32(dt), f32(A), B.contiguous(), C.contiguous(),
+                                       f32(D), None if z is None else z.contiguous(),
+                                       f32(norm_weight) if z is not None else None, init, cu)
+    return (out, final) if return_final_state else out

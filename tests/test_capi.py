@@ -1,0 +1,161 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the header
+declares, the ctypes layouts match the C structs, and host-side validation
+returns the documented status for each bad descriptor (no GPU calls)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ssd_mi355x.h"
+
+
+@pytest.fixture(scope="module")
+def capi():
+    from kernels import _capi
+    _capi.load()
+    return _capi
+
+
+def _header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(ssd_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(capi):
+    declared = _header_functions()
+    assert set(declared) == set(capi.EXPORTS), declared
+    lib = ctypes.CDLL(str(capi.LIB_PATH))
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert capi.load().ssd_abi_version() == capi.ABI_VERSION
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_ctypes_layout_matches_header(tmp_path, capi):
+    src = tmp_path / "layout.c"
+    fields = {
+        "ssd_desc_t": [f[0] for f in capi.SsdDesc._fields_],
+        "ssd_fwd_args_t": [f[0] for f in capi.SsdFwdArgs._fields_],
+        "ssd_bwd_args_t": [f[0] for f in capi.SsdBwdArgs._fields_],
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for st, fs in fields.items():
+        lines.append(f'printf("{st} %zu\\n", sizeof({st}));')
+        for f in fs:
+            lines.append(f'printf("{st}.{f} %zu\\n", offsetof({st}, {f}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
+    out = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                          check=True).stdout.splitlines())
+    for st, cls in (("ssd_desc_t", capi.SsdDesc), ("ssd_fwd_args_t", capi.SsdFwdArgs),
+                    ("ssd_bwd_args_t", capi.SsdBwdArgs)):
+        assert int(out[st]) == ctypes.sizeof(cls), st
+        for f in fields[st]:
+            assert int(out[f"{st}.{f}"]) == getattr(cls, f).offset, f"{st}.{f}"
+
+
+def _desc(capi, **kw):
+    d = capi.SsdDesc()
+    base = dict(batch=4, seqlen=8192, nheads=64, headdim=64, ngroups=1, dstate=128, chunk=256,
+                dtype=capi.SSD_DTYPE_BF16, state_dtype=capi.SSD_DTYPE_F32, a_mode=capi.SSD_A_PER_HEAD,
+                has_dt=1, has_D=1, has_z=1, want_final=1, norm_eps=1e-6)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(d, k, v)
+    return d
+
+
+def _validate(capi, **kw):
+    return capi.load().ssd_validate(ctypes.byref(_desc(capi, **kw)))
+
+
+def test_validation_accepts_benchmark_configs(capi):
+    assert _validate(capi) == capi.SSD_OK                                     # config 2
+    assert _validate(capi, batch=8, seqlen=2048, nheads=24, has_z=0) == capi.SSD_OK  # config 1
+    assert _validate(capi, batch=1, seqlen=65536, nheads=32, ngroups=8, dstate=64, varlen=1, nseq=15,
+                     has_init=1) == capi.SSD_OK                               # config 3
+    assert _validate(capi, batch=1, seqlen=512, nheads=4, headdim=32, dstate=32, chunk=64,
+                     dtype=capi.SSD_DTYPE_F32, has_z=0) == capi.SSD_OK        # config 0
+    # reference API: per-token A, no dt, state in the input dtype
+    assert _validate(capi, a_mode=capi.SSD_A_PER_TOKEN, has_dt=0, has_D=0, has_z=0, ngroups=64,
+                     state_dtype=capi.SSD_DTYPE_BF16, want_A_cumsum=1) == capi.SSD_OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(batch=0), "SSD_ERR_INVALID"),
+    (dict(nheads=6, ngroups=4), "SSD_ERR_INVALID"),
+    (dict(dtype=7), "SSD_ERR_INVALID"),
+    (dict(a_mode=1, has_dt=1), "SSD_ERR_INVALID"),
+    (dict(varlen=1, nseq=3), "SSD_ERR_INVALID"),                 # varlen needs batch == 1
+    (dict(a_mode=2, has_dt=0, seqlen=8000), "SSD_ERR_INVALID"),  # cumsum path needs T % Q == 0
+    (dict(want_A_cumsum=1, varlen=1, batch=1, nseq=2), "SSD_ERR_INVALID"),
+    (dict(norm_eps=float("nan")), "SSD_ERR_INVALID"),
+    (dict(chunk=512), "SSD_ERR_UNSUPPORTED"),
+    (dict(headdim=256), "SSD_ERR_UNSUPPORTED"),
+    (dict(dstate=160), "SSD_ERR_UNSUPPORTED"),
+    (dict(dtype=0), "SSD_ERR_UNSUPPORTED"),                      # fp32 tiles exceed LDS at N=128, P=64
+])
+def test_validation_rejects(capi, kw, status):
+    assert _validate(capi, **kw) == getattr(capi, status)
+
+
+def test_workspace_sizes(capi):
+    lib = capi.load()
+    d = _desc(capi)
+    saved = lib.ssd_workspace_bytes(ctypes.byref(d), capi.SSD_WS_SAVED)
+    fwd = lib.ssd_workspace_bytes(ctypes.byref(d), capi.SSD_WS_FWD_SCRATCH)
+    bwd = lib.ssd_workspace_bytes(ctypes.byref(d), capi.SSD_WS_BWD_SCRATCH)
+    # saved: bf16 chunk-entering states (b*c*h*P*N*2) + y before the norm (b*L*H*P*2) + small
+    assert saved >= 4 * 32 * 64 * 64 * 128 * 2 + 4 * 8192 * 64 * 64 * 2
+    assert fwd == 4 * 32 * 64 * 64 * 128 * 4
+    assert bwd > fwd
+    assert lib.ssd_workspace_bytes(ctypes.byref(_desc(capi, batch=0)), 0) == 0
+
+
+def test_entry_points_reject_null_pointers_without_touching_the_gpu(capi):
+    lib = capi.load()
+    d = _desc(capi)
+    args = capi.SsdFwdArgs()
+    assert lib.ssd_fwd(ctypes.byref(d), ctypes.byref(args), None, 0, None, 0, None) == capi.SSD_ERR_INVALID
+    bargs = capi.SsdBwdArgs()
+    assert lib.ssd_bwd(ctypes.byref(d), ctypes.byref(bargs), None, 0, None, 0, None) == capi.SSD_ERR_INVALID
+    # pointers present but workspace missing -> workspace error
+    fake = ctypes.c_void_p(16)
+    args = capi.SsdFwdArgs(fake, fake, fake, fake, fake, fake, fake, fake, None, None, fake, fake, None)
+    assert lib.ssd_fwd(ctypes.byref(d), ctypes.byref(args), None, 0, None, 0, None) == capi.SSD_ERR_WORKSPACE
+    assert lib.ssd_status_string(capi.SSD_ERR_WORKSPACE) == b"workspace missing or too small"
+
+
+def test_python_layer_maps_status_to_exceptions(capi):
+    with pytest.raises(ValueError):
+        capi.check(capi.SSD_ERR_INVALID, "x")
+    with pytest.raises(NotImplementedError):
+        capi.check(capi.SSD_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        capi.check(capi.SSD_ERR_HIP, "x")
+
+
+def test_product_path_refuses_cpu_tensors():
+    import torch
+    import kernels
+    x = torch.randn(1, 64, 2, 8)
+    A = -torch.rand(1, 64, 2) * 0.1
+    B = torch.randn(1, 64, 2, 4)
+    with pytest.raises(AssertionError):
+        kernels.fused_ssd_scan(x, A, B, B, 32)
+    with pytest.raises(AssertionError):
+        kernels.ssd_scan_combined(x, A.abs(), -torch.ones(2), B, B, 32)
+
+
+def test_product_path_never_imports_the_oracle():
+    pkg = ROOT / "dhammic-ai_amd"
+    for f in pkg.rglob("*.py"):
+        assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", f.read_text(), re.M), f

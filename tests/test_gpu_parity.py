@@ -1,0 +1,254 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs. Tolerances from BASELINE's north_star, normwise per tensor
+(max|got - ref| / max|ref|): 1e-4 for fp32 inputs, 1e-2 for bf16 inputs
+(the oracle then runs in fp64 on the bf16-rounded values)."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from oracle.inputs import SsdShape, make_inputs, make_reference_test_inputs
+from ssd_testlib import TOL, assert_close, oracle_extended, oracle_reference_api
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs an MI355X (HIP device)")]
+
+DEV = "cuda"
+
+
+def _k():
+    import kernels
+    return kernels
+
+
+def _to(t, dtype):
+    return t.to(dtype).to(DEV)
+
+
+# --------------------------------------------------------------------------- #
+# Reference API (fused_ssd_scan / FusedSSDScan), the reference test's shapes
+# (r2/dhammic-ai/tests/kernels/test_ssd_scan.py:42-174)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("shape", [(2, 512, 4, 32, 8), (2, 256, 4, 16, 8), (1, 1024, 4, 16, 8),
+                                   (2, 512, 8, 32, 8)])
+def test_reference_shapes_fp32(shape):
+    b, T, h, p, n = shape
+    chunk = 128
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=0)
+    dY = torch.randn(b, T, h, p, generator=torch.Generator().manual_seed(1))
+    Yo, fo, go, _ = oracle_reference_api(x, A, B, C, chunk, dY)
+    xs, As, Bs, Cs = [_to(t, torch.float32).requires_grad_(True) for t in (x, A, B, C)]
+    Y, fs, cache = _k().fused_ssd_scan(xs, As, Bs, Cs, chunk_size=chunk)
+    Y.backward(dY.to(DEV))
+    tol = TOL[torch.float32]
+    assert Y.shape == (b, T, h, p) and fs.shape == (b, h, p, n)
+    assert_close("Y", Y, Yo, tol)
+    assert_close("final_state", fs, fo, tol)
+    for name, t in (("dx", xs), ("dA", As), ("dB", Bs), ("dC", Cs)):
+        assert_close(name, t.grad, go[name[1:]], tol)
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 256])
+def test_reference_bf16(chunk):
+    b, T, h, p, n = 2, 512, 4, 32, 8
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=2)
+    x, A, B, C = [t.bfloat16().float() for t in (x, A, B, C)]
+    dY = torch.randn(b, T, h, p, generator=torch.Generator().manual_seed(3)).bfloat16().float()
+    Yo, fo, go, _ = oracle_reference_api(x, A, B, C, chunk, dY)
+    xs, As, Bs, Cs = [_to(t, torch.bfloat16).requires_grad_(True) for t in (x, A, B, C)]
+    Y, fs, _ = _k().fused_ssd_scan(xs, As, Bs, Cs, chunk)
+    Y.backward(dY.to(DEV, torch.bfloat16))
+    tol = TOL[torch.bfloat16]
+    assert Y.dtype == torch.bfloat16 and fs.dtype == torch.bfloat16
+    assert_close("Y", Y, Yo, tol)
+    assert_close("final_state", fs, fo, tol)
+    for name, t in (("dx", xs), ("dA", As), ("dB", Bs), ("dC", Cs)):
+        assert_close(name, t.grad, go[name[1:]], tol)
+
+
+def test_reference_cache_contract_and_values():
+    """test_ssd_scan.py:99-131: cache shapes, reuse equality; plus the cache
+    tensors' values against the oracle and the dropped dA of the cache path."""
+    b, T, h, p, n, chunk = 2, 512, 4, 32, 8, 128
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=4)
+    x2, _, B2, C2 = make_reference_test_inputs(b, T, h, p, n, seed=5)
+    k = _k()
+    g = [_to(t, torch.float32) for t in (x, A, B, C)]
+    _, fs, cache = k.fused_ssd_scan(*g, chunk_size=chunk)
+    c = T // chunk
+    assert cache["L"].shape == (b, h, c, chunk, chunk)
+    assert cache["decay_chunk"].shape == (b, h, c + 1, c + 1)
+    assert cache["A_cumsum"].shape == (b, h, c, chunk)
+    _, _, _, cache_o = oracle_reference_api(x, A, B, C, chunk, torch.zeros(b, T, h, p))
+    for key in ("L", "decay_chunk", "A_cumsum"):
+        assert_close(key, cache[key], cache_o[key], 1e-5)
+    x2g, B2g, C2g = [_to(t, torch.float32) for t in (x2, B2, C2)]
+    Yf, ff, _ = k.fused_ssd_scan(x2g, g[1], B2g, C2g, chunk_size=chunk)
+    x2l, Al, B2l, C2l = [t.clone().requires_grad_(True) for t in (x2g, g[1], B2g, C2g)]
+    Yr, fr, _ = k.fused_ssd_scan(x2l, Al, B2l, C2l, chunk_size=chunk, cache=cache)
+    assert (Yr - Yf).abs().max().item() < 1e-4 and (fr - ff).abs().max().item() < 1e-4
+    dY = torch.randn(b, T, h, p, generator=torch.Generator().manual_seed(6))
+    Yr.backward(dY.to(DEV))
+    assert Al.grad is None
+    _, _, go, _ = oracle_reference_api(x2, A, B2, C2, chunk, dY, cache_from=(x, A, B, C))
+    assert go["A"] is None
+    for name, t in (("dx", x2l), ("dB", B2l), ("dC", C2l)):
+        assert_close(name, t.grad, go[name[1:]], TOL[torch.float32])
+
+
+def test_reference_initial_state_and_final_grad():
+    b, T, h, p, n, chunk = 2, 256, 4, 16, 8, 64
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=7)
+    gen = torch.Generator().manual_seed(8)
+    init = torch.randn(b, 1, h, p, n, generator=gen) * 0.1
+    dY = torch.randn(b, T, h, p, generator=gen)
+    dF = torch.randn(b, h, p, n, generator=gen)
+    Yo, fo, go, _ = oracle_reference_api(x, A, B, C, chunk, dY, init=init, dfinal=dF)
+    xs, As, Bs, Cs, ins = [_to(t, torch.float32).requires_grad_(True) for t in (x, A, B, C, init)]
+    Y, fs, _ = _k().fused_ssd_scan(xs, As, Bs, Cs, chunk, initial_states=ins)
+    torch.autograd.backward([Y, fs], [dY.to(DEV), dF.to(DEV)])
+    tol = TOL[torch.float32]
+    assert_close("Y", Y, Yo, tol)
+    assert_close("final_state", fs, fo, tol)
+    for name, t in (("dx", xs), ("dA", As), ("dB", Bs), ("dC", Cs)):
+        assert_close(name, t.grad, go[name[1:]], tol)
+    assert ins.grad.shape == (b, 1, h, p, n)
+    assert_close("dinit", ins.grad, go["init"], tol)
+
+
+def test_fused_ssd_scan_autograd_function_contract():
+    """FusedSSDScan.apply: 9 inputs, 5 outputs, same values as fused_ssd_scan."""
+    b, T, h, p, n, chunk = 1, 256, 2, 16, 8, 64
+    x, A, B, C = [_to(t, torch.float32) for t in make_reference_test_inputs(b, T, h, p, n, seed=9)]
+    k = _k()
+    Y1, f1, cache = k.fused_ssd_scan(x, A, B, C, chunk)
+    out = k.FusedSSDScan.apply(x, A, B, C, chunk, None, None, None, None)
+    assert len(out) == 5
+    assert (out[0] - Y1).abs().max().item() == 0.0
+    assert (out[1] - f1).abs().max().item() == 0.0
+    assert (out[2] - cache["L"]).abs().max().item() == 0.0
+
+
+def test_reference_errors():
+    k = _k()
+    x, A, B, C = [_to(t, torch.float32) for t in make_reference_test_inputs(1, 100, 2, 8, 4)]
+    with pytest.raises(AssertionError):
+        k.fused_ssd_scan(x, A, B, C, 64)
+    with pytest.raises(AssertionError):
+        k.fused_ssd_scan(x.cpu(), A.cpu(), B.cpu(), C.cpu(), 50)
+
+
+# --------------------------------------------------------------------------- #
+# Extended API (dt, per-head A, groups, D, gated norm, init/final, varlen)
+# --------------------------------------------------------------------------- #
+def _ext_inputs(shape, seed, dtype, with_z):
+    inp = make_inputs(shape, seed=seed, with_z=with_z, with_init=True, with_dfinal=True)
+    for k in ("x", "B", "C", "dy", "z"):
+        if k in inp:
+            inp[k] = inp[k].to(dtype).float()   # rounded to the test dtype
+    return inp
+
+
+def _run_ext(inp, shape, dtype, with_z, cu=None, use_init=True, use_dfinal=True, norm_weight=None):
+    dev = {k: v.to(DEV) for k, v in inp.items()}
+    leaves = {}
+    for k in ("x", "B", "C", "z"):
+        if k in dev:
+            leaves[k] = dev[k].to(dtype).requires_grad_(True)
+    for k in ("dt", "A", "D", "init"):
+        leaves[k] = dev[k].requires_grad_(True)
+    w = None if norm_weight is None else norm_weight.to(DEV).requires_grad_(True)
+    out, fin = _k().ssd_scan_combined(
+        leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], shape.chunk, D=leaves["D"],
+        z=leaves.get("z") if with_z else None, norm_weight=w,
+        initial_states=leaves["init"] if use_init else None,
+        cu_seqlens=None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV),
+        return_final_state=True)
+    outs, grads = [out], [dev["dy"].to(dtype)]
+    if use_dfinal:
+        outs.append(fin)
+        grads.append(dev["dfinal"])
+    torch.autograd.backward(outs, grads)
+    g = {k: v.grad for k, v in leaves.items()}
+    g["w"] = None if w is None else w.grad
+    return out, fin, g
+
+
+def _check_ext(shape, dtype, with_z, seed=0, cu=None, use_init=True, use_dfinal=True, randw=False):
+    inp = _ext_inputs(shape, seed, dtype, with_z)
+    nw = None
+    if with_z:
+        nw = torch.ones(shape.nheads * shape.headdim)
+        if randw:
+            nw = nw + 0.1 * torch.randn(shape.nheads * shape.headdim, generator=torch.Generator().manual_seed(seed))
+    out, fin, g = _run_ext(inp, shape, dtype, with_z, cu, use_init, use_dfinal, nw)
+    oo, fo, go = oracle_extended(inp, shape.chunk, with_z=with_z, init=inp["init"] if use_init else None,
+                                 cu=None if cu is None else torch.tensor(cu), dfinal=inp["dfinal"] if use_dfinal else None,
+                                 norm_weight=nw)
+    tol = TOL[dtype]
+    errs = {"out": assert_close("out", out, oo, tol), "final": assert_close("final", fin, fo, tol)}
+    names = ["x", "dt", "A", "B", "C", "D"] + (["z"] if with_z else []) + (["init"] if use_init else [])
+    for k in names:
+        errs["d" + k] = assert_close("d" + k, g[k], go[k], tol)
+    if with_z:
+        errs["dw"] = assert_close("dw", g["w"], go["w"], tol)
+    return errs
+
+
+def test_extended_config0_fp32():
+    """BASELINE config 0 shape (the CPU-baseline case), fp32, all features but z."""
+    _check_ext(SsdShape(1, 512, 4, 32, 1, 32, 64), torch.float32, with_z=False)
+
+
+def test_extended_config0_fp32_gated():
+    _check_ext(SsdShape(1, 512, 4, 32, 1, 32, 64), torch.float32, with_z=True, randw=True)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4])
+def test_extended_bf16_groups(G):
+    _check_ext(SsdShape(2, 1024, 8, 64, G, 64, 256), torch.bfloat16, with_z=False, seed=G)
+
+
+def test_extended_bf16_gated_130m_slice():
+    """Config 1's per-head dims (P=64, N=128, Q=256) on a slice of its batch/heads."""
+    _check_ext(SsdShape(2, 1024, 6, 64, 1, 128, 256), torch.bfloat16, with_z=True, seed=11)
+
+
+def test_extended_varlen_ragged_fp32():
+    """Packed sequences with partial chunks and an empty sequence; state reset at
+    every boundary; per-sequence initial/final states and their gradients."""
+    lens = [100, 64, 0, 257, 31, 60]
+    cu = [0]
+    for v in lens:
+        cu.append(cu[-1] + v)
+    shape = SsdShape(1, cu[-1], 4, 16, 2, 16, 64, cu_seqlens=cu)
+    _check_ext(shape, torch.float32, with_z=False, seed=12, cu=cu)
+
+
+def test_extended_varlen_bf16_config3_like():
+    """Config 3's per-head dims (H=32 is cut to 8, G=8 -> 4) on ~6k packed tokens."""
+    lens = [1500, 777, 2048, 513, 1200]
+    cu = [0]
+    for v in lens:
+        cu.append(cu[-1] + v)
+    shape = SsdShape(1, cu[-1], 8, 64, 4, 64, 256, cu_seqlens=cu)
+    _check_ext(shape, torch.bfloat16, with_z=False, seed=13, cu=cu)
+
+
+def test_extended_partial_last_chunk_no_init():
+    """seqlen not a chunk multiple (the caller's zero-pad case), no init, no dfinal."""
+    _check_ext(SsdShape(2, 300, 4, 32, 1, 32, 128), torch.float32, with_z=False, seed=14,
+               use_init=False, use_dfinal=False)
+
+
+def test_backward_is_deterministic():
+    shape = SsdShape(2, 1024, 8, 64, 1, 128, 256)
+    inp = _ext_inputs(shape, 15, torch.bfloat16, True)
+    r1 = _run_ext(inp, shape, torch.bfloat16, True)
+    r2 = _run_ext(inp, shape, torch.bfloat16, True)
+    for k in ("x", "dt", "A", "B", "C", "D", "z", "init"):
+        assert torch.equal(r1[2][k], r2[2][k]), k
+    assert torch.equal(r1[0], r2[0])
