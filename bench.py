@@ -1,0 +1,245 @@
+#!/usr/bin/env python
+"""SSD scan fwd+bwd throughput on one MI355X, with the dominant kernel's
+roofline and the reference CPU path timed on the host beside it.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+
+A step is one forward + backward of the fused chunked SSD scan over the
+1.3B-class layer: B=4, L=8192, H=64, P=64, G=1, N=128,
+chunk 256, bf16 x/B/C/z/dy, fp32 dt/A/D, + D*x and the gated RMSNorm
+epilogue. Inputs are synthetic (the configs' distributions), generated on the
+GPU and resident in HBM before timing starts. Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "dhammic-ai_amd"))
+
+METRIC = "SSD scan fwd+bwd Mtokens/s at 1.3B-layer shape + % of MFMA/HBM roofline"
+CFG = dict(batch=4, seqlen=8192, nheads=64, headdim=64, ngroups=1, dstate=128, chunk=256)
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+
+
+def make_inputs(dev, seed=2):
+    """BASELINE distributions, drawn on the GPU."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator(device=dev).manual_seed(seed)
+    b, L, H, P, G, N = (CFG[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate"))
+    kw = dict(generator=g, device=dev, dtype=torch.float32)
+    bf = torch.bfloat16
+    t = {
+        "x": torch.randn(b, L, H, P, **kw).to(bf),
+        "dt": F.softplus(torch.randn(b, L, H, **kw) - 4.0).clamp(1e-3, 0.1),
+        "A": -torch.exp(torch.rand(H, **kw) * math.log(16.0)),
+        "B": (torch.randn(b, L, G, N, **kw) / math.sqrt(N)).to(bf),
+        "C": (torch.randn(b, L, G, N, **kw) / math.sqrt(N)).to(bf),
+        "D": torch.randn(H, **kw),
+        "z": torch.randn(b, L, H, P, **kw).to(bf),
+        "w": torch.ones(H * P, device=dev, dtype=torch.float32),
+        "dy": torch.randn(b, L, H, P, **kw).to(bf),
+    }
+    return t
+
+
+def phase_models(nchunks):
+    """Algorithmic FLOPs (matrix contractions, causal count, no recompute credit)
+    and logical HBM bytes (each input read once, each output written once) per
+    launch of each phase, at the bench config. Per-token FLOP terms follow the
+    fwd+bwd split F_tok = H(3(Q+1)P + 12NP) + 3G(Q+1)N."""
+    b, L, H, P, G, N, Q = (CFG[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate",
+                                            "chunk"))
+    R = b * L
+    es = 2
+    x = R * H * P * es          # x, y, z, dy, dx, dz, y_pre, dy_pre: one bf16 (R,H,P) tensor
+    bc = R * G * N * es         # B or C
+    dt = R * H * 4
+    st32 = nchunks * H * P * N * 4
+    st16 = nchunks * H * P * N * es
+    cs = nchunks * H * Q * 4
+    m = {
+        "fwd_state": (R * H * 2 * N * P, x + bc + dt + cs + st32),
+        "fwd_pass": (0, st32 + st16 + cs),
+        "fwd_scan": (R * (G * (Q + 1) * N + H * ((Q + 1) * P + 2 * N * P)), 2 * x + 2 * bc + dt + cs + st16),
+        "norm_fwd": (0, 3 * x + R * 4),
+        "norm_bwd": (0, 5 * x + R * 4),
+        "bwd_state": (R * H * 2 * N * P, x + bc + cs + st32),
+        "bwd_pass": (0, 2 * st32 + st16 + cs),
+        "bwd_col": (R * (H * (2 * (Q + 1) * P + 4 * N * P) + G * (Q + 1) * N),
+                    3 * x + 2 * bc + dt + cs + st32),
+        "bwd_row": (R * (H * 2 * N * P + G * (Q + 1) * N), 2 * x + 3 * bc + dt + cs + st16),
+    }
+    return m
+
+
+def time_gpu(steps, warmup):
+    import torch
+    from kernels import _capi as C_
+    from kernels import ssd_scan as S
+
+    dev = torch.device("cuda", 0)
+    t = make_inputs(dev)
+    cfg = S._Cfg(chunk=CFG["chunk"], a_mode=C_.SSD_A_PER_HEAD, nseq=CFG["batch"], varlen=False,
+                 state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=1e-6)
+    NP = C_.SSD_NUM_PHASES
+    EvArr = ctypes.c_void_p * (2 * NP)
+
+    def one_step(ev_arr=None):
+        y, final, _, saved = S._forward(cfg, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["z"], t["w"],
+                                        None, None, ev_arr)
+        S._backward(cfg, saved, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["z"], t["w"], None, None,
+                    t["dy"], None, ev_arr)
+        return y
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+
+    # per-step event sets (created by a first record so the handles exist)
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * NP)] for _ in range(steps)]
+    for row in ev:
+        for e in row:
+            e.record(stream)
+    arrs = [EvArr(*[ctypes.c_void_p(e.cuda_event) for e in row]) for row in ev]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        one_step(arrs[i])
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = start.elapsed_time(stop)
+    phases = {}
+    for k, name in enumerate(C_.PHASES):
+        vals = []
+        for row in ev:
+            try:
+                vals.append(row[2 * k].elapsed_time(row[2 * k + 1]))
+            except RuntimeError:
+                vals = []
+                break
+        # a phase that did not run keeps the two initial records: ~0 ms apart
+        if vals and max(vals) > 0.0005:
+            phases[name] = statistics.mean(vals)
+    # the same event pairs bracket the fwd_scan / bwd kernels of every step; also
+    # count chunks for the models
+    nchunks = CFG["batch"] * math.ceil(CFG["seqlen"] / CFG["chunk"])
+    return ms_total / steps, wall / steps * 1e3, phases, nchunks
+
+
+def roofline(phases, nchunks):
+    models = phase_models(nchunks)
+    name = max(phases, key=lambda k: phases[k])
+    flops, nbytes = models.get(name, (0, 0))
+    t_s = phases[name] * 1e-3
+    intensity = flops / nbytes if nbytes else 0.0
+    if intensity > RIDGE:
+        achieved = flops / t_s / 1e12
+        out = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        achieved = nbytes / t_s / 1e9
+        out = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    out["frac"] = out["achieved"] / out["peak"]
+    out["kernel"] = name
+    out["kernel_ms"] = phases[name]
+    out["algorithmic_flops"] = flops
+    out["algorithmic_bytes"] = nbytes
+    out["traffic"] = None
+    return out
+
+
+def cpu_baseline():
+    """The reference's chunked PyTorch path (oracle restatement of
+    r2/dhammic-ai/src/kernels/ssd_scan.py:330-533), fp32, timed on host cores:
+    forward under no_grad, backward = re-run forward + autograd.grad (the
+    FusedSSDScan pattern). Sample: one batch row, 8 of config 2's 64 heads,
+    L=2048 (8 chunks), P=64, N=128, Q=256; tokens/s scaled to all 64 heads."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import ssd_chunked as oc
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    b, L, Hs, P, N, Q = 1, 2048, 8, CFG["headdim"], CFG["dstate"], CFG["chunk"]
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(b, L, Hs, P, generator=g)
+    dt = torch.nn.functional.softplus(torch.randn(b, L, Hs, generator=g) - 4.0).clamp(1e-3, 0.1)
+    A = -torch.exp(torch.rand(Hs, generator=g) * math.log(16.0))
+    Bm = (torch.randn(b, L, 1, N, generator=g) / math.sqrt(N)).expand(b, L, Hs, N).contiguous()
+    Cm = (torch.randn(b, L, 1, N, generator=g) / math.sqrt(N)).expand(b, L, Hs, N).contiguous()
+    dY = torch.randn(b, L, Hs, P, generator=g)
+    X, a = x * dt[..., None], dt * A
+    times = []
+    budget = 12.0
+    t_all = time.perf_counter()
+    for i in range(2 + 30):
+        t0 = time.perf_counter()
+        oc.fused_ssd_scan_fwd_bwd_baseline(X, a, Bm, Cm, Q, dY)
+        dtime = time.perf_counter() - t0
+        if i >= 2:
+            times.append(dtime)
+        if time.perf_counter() - t_all > budget and len(times) >= 3:
+            break
+    med = statistics.median(times)
+    scale = CFG["nheads"] / Hs
+    mtok = b * L / (med * scale) / 1e6
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:
+        model = "unknown"
+    return {"value": mtok, "unit": "Mtokens/s", "cores": cores, "kind": "port",
+            "sample": f"reference chunked path (oracle restatement), fp32, fwd+bwd, B=1 L={L} H={Hs} of 64 "
+                      f"P={P} N={N} Q={Q}; median of {len(times)} iterations ({med*1e3:.1f} ms); "
+                      f"tokens/s scaled by {Hs}/64 heads; cpu: {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); the SSD scan is sharded "
+              "across GPUs by batch/heads with no communication, so N GPUs run N independent copies.",
+              file=sys.stderr)
+        sys.exit(2)
+    rank = int(os.environ.get("RANK", "0"))
+    ms_step, wall_ms, phases, nchunks = time_gpu(a.steps, a.warmup)
+    tokens = CFG["batch"] * CFG["seqlen"]
+    value = tokens / (ms_step * 1e-3) / 1e6
+    rl = roofline(phases, nchunks)
+    out = {
+        "metric": METRIC, "value": value, "unit": "Mtokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "config 2: 1.3B-class SSD layer fwd+bwd with D and gated RMSNorm", **CFG,
+                   "x_dtype": "bf16", "state_dtype": "fp32", "tokens_per_step": tokens},
+        "roofline": rl,
+        "kernels_ms": {k: round(v, 4) for k, v in phases.items()},
+        "wall_ms_per_step": wall_ms,
+    }
+    if rank == 0 and not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    if rank == 0:
+        print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -90,8 +90,9 @@ def _check_device(*ts):
             raise AssertionError("fused SSD scan: all tensors must be on the GPU (got a CPU tensor)")
 
 
-def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu):
-    """Run ssd_fwd. Returns (y, final_state, A_cumsum_out or empty, saved workspace)."""
+def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None):
+    """Run ssd_fwd. Returns (y, final_state, A_cumsum_out or empty, saved workspace).
+    ``events``: optional ctypes array of 2*SSD_NUM_PHASES hipEvent_t (profiling)."""
     lib = C_.load()
     _check_device(x, dt, A, B, C, D, z, w, init, cu)
     desc = _desc(cfg, x, B, dt, D, z, init)
@@ -109,7 +110,8 @@ def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu):
     scratch = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_FWD_SCRATCH),
                           dtype=torch.uint8, device=dev)
     args = C_.SsdFwdArgs(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(w), _p(init), _p(cu),
-                         _p(y), _p(final), _p(acs) if cfg.want_acs else None)
+                         _p(y), _p(final), _p(acs) if cfg.want_acs else None,
+                         None if events is None else ctypes.cast(events, ctypes.c_void_p))
     with torch.cuda.device(dev):
         st = lib.ssd_fwd(ctypes.byref(desc), ctypes.byref(args), _p(saved), saved.numel(), _p(scratch),
                          scratch.numel(), _stream(dev))
@@ -117,7 +119,7 @@ def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu):
     return y, final, acs, saved
 
 
-def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal):
+def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal, events=None):
     """Run ssd_bwd. Returns dict of gradients (None where the input is absent)."""
     lib = C_.load()
     desc = _desc(cfg, x, B, dt, D, z, init, has_dfinal=dfinal is not None)
@@ -142,7 +144,8 @@ def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal
     args = C_.SsdBwdArgs(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(w), _p(init), _p(cu),
                          _p(dy), _p(dfinal),
                          _p(g["x"]), _p(g["dt"]), _p(g["A"]), _p(g["B"]), _p(g["C"]), _p(g["D"]),
-                         _p(g["z"]), _p(g["w"]), _p(g["init"]))
+                         _p(g["z"]), _p(g["w"]), _p(g["init"]),
+                         None if events is None else ctypes.cast(events, ctypes.c_void_p))
     with torch.cuda.device(dev):
         st = lib.ssd_bwd(ctypes.byref(desc), ctypes.byref(args), _p(saved_ws), saved_ws.numel(), _p(scratch),
                          scratch.numel(), _stream(dev))
