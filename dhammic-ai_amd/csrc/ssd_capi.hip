@@ -1,6 +1,8 @@
 // extern "C" entry points: validation, workspace layout, launch sequences.
 #include <string.h>
 
+#include <initializer_list>
+
 #include "../../include/ssd_mi355x.h"
 #include "ssd_launch.h"
 
@@ -54,7 +56,10 @@ int plan(const ssd_desc_t* s, Plan* p) {
   SsdDims& d = p->d;
   d.batch = (int)s->batch; d.seqlen = (int)s->seqlen; d.H = (int)s->nheads; d.P = (int)s->headdim;
   d.G = (int)s->ngroups; d.N = (int)s->dstate; d.Q = (int)s->chunk;
-  d.Ppad = round_up(d.P, 32); d.Npad = round_up(d.N, 32); d.Qpad = round_up(d.Q, SSD_BLK);
+  // feature widths padded to 32, 64 or 128 (the tile shapes the kernels are built for)
+  d.Ppad = d.P <= 32 ? 32 : (d.P <= 64 ? 64 : 128);
+  d.Npad = d.N <= 32 ? 32 : (d.N <= 64 ? 64 : 128);
+  d.Qpad = round_up(d.Q, SSD_BLK);
   d.nseq = (int)nseq; d.max_chunks = (int)max_chunks; d.hpg = d.H / d.G; d.R = R;
   d.a_mode = s->a_mode; d.has_dt = s->has_dt != 0; d.has_D = s->has_D != 0; d.has_z = s->has_z != 0;
   d.has_init = s->has_init != 0; d.has_dfinal = s->has_dfinal != 0; d.varlen = s->varlen != 0;
@@ -139,6 +144,20 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
 }
 
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Vector-load flags for this call: widths and row strides multiples of one
+// 16-byte vector, every pointer of that shape 16-byte aligned.
+void set_vec_flags(SsdDims* d, int dtype, std::initializer_list<const void*> xs,
+                   std::initializer_list<const void*> bcs) {
+  const int V = dtype == SSD_DTYPE_BF16 ? 8 : 4;
+  bool vx = d->P % V == 0, vbc = d->N % V == 0;
+  for (const void* p : xs) vx = vx && aligned16(p);
+  for (const void* p : bcs) vbc = vbc && aligned16(p);
+  d->vec_x = vx;
+  d->vec_bc = vbc;
+}
+
 #define SSD_TRY(expr)                          \
   do {                                         \
     if ((expr) != hipSuccess) return SSD_ERR_HIP; \
@@ -188,7 +207,7 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
   Plan p;
   int st = plan(desc, &p);
   if (st != SSD_OK) return st;
-  const SsdDims& d = p.d;
+  SsdDims& d = p.d;
   if (!a || !a->x || !a->A || !a->B || !a->C || !a->y) return SSD_ERR_INVALID;
   if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight)) ||
       (d.has_init && !a->init) || (d.varlen && !a->cu_seqlens) || (desc->want_final && !a->final_state) ||
@@ -196,6 +215,7 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
     return SSD_ERR_INVALID;
   if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.fwd_bytes) return SSD_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  set_vec_flags(&p.d, p.dtype, {a->x, a->y, a->z}, {a->B, a->C});
   SsdBufs b;
   memset(&b, 0, sizeof(b));
   bind_saved(p, saved, &b);
@@ -219,13 +239,14 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   Plan p;
   int st = plan(desc, &p);
   if (st != SSD_OK) return st;
-  const SsdDims& d = p.d;
+  SsdDims& d = p.d;
   if (!a || !a->x || !a->A || !a->B || !a->C || !a->dy || !a->dx || !a->dB || !a->dC) return SSD_ERR_INVALID;
   if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight || !a->dz)) ||
       (d.varlen && !a->cu_seqlens) || (d.has_dfinal && !a->dfinal))
     return SSD_ERR_INVALID;
   if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.bwd_bytes) return SSD_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  set_vec_flags(&p.d, p.dtype, {a->x, a->z, a->dy, a->dx, a->dz}, {a->B, a->C, a->dB, a->dC});
   SsdBufs b;
   memset(&b, 0, sizeof(b));
   bind_saved(p, const_cast<void*>(saved), &b);

@@ -22,6 +22,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #define SSD_WAVE 64
+// Rows of the token axis per block tile inside a chunk.
+#define SSD_BLK 64
 #define SSD_LO (-20.0f)
 #define SSD_HI (20.0f)
 
@@ -107,6 +109,96 @@ __device__ __forceinline__ void mma_tile(floatx16& acc, const T* a, int lda, con
   }
 }
 
+// ---------------------------------------------------------------------------
+// Accumulator tile reused as an MFMA A operand (no LDS round trip).
+// A 32x32 fp32 tile X in accumulator layout (lane: column b = lane%32; rows
+// a = 8r + 4*(lane/32) + q in register 4r + q) serves as A'[i = b][k = a],
+// i.e. A' = X^T. K-step kk (0 or 1) covers rows a = 16kk .. 16kk+15 of X,
+// registers 8kk .. 8kk+7; their row order is a = 16kk + 8*(t/4) + 4*(lane/32)
+// + t%4 for t = 0..7, so the B operand is read in the same permuted order.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> __device__ __forceinline__ Frag<T> frag_from_acc(const floatx16& x, int kk);
+template <> __device__ __forceinline__ Frag<bf16> frag_from_acc<bf16>(const floatx16& x, int kk) {
+  Frag<bf16> f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) f.v[t] = (bf16)x[8 * kk + t];
+  return f;
+}
+template <> __device__ __forceinline__ Frag<float> frag_from_acc<float>(const floatx16& x, int kk) {
+  Frag<float> f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) f.v[t] = x[8 * kk + t];
+  return f;
+}
+
+// B'[a][j] for the permuted rows a of step kk, from row j of a [j][a] tile (a contiguous).
+__device__ __forceinline__ Frag<bf16> ld_frag_perm(const bf16* row, int kk) {
+  const int off = 16 * kk + 4 * (lane_id() >> 5);
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + off);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + off + 8);
+  Frag<bf16> f;
+  f.v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return f;
+}
+__device__ __forceinline__ Frag<float> ld_frag_perm(const float* row, int kk) {
+  const int off = 16 * kk + 4 * (lane_id() >> 5);
+  const floatx4 lo = *reinterpret_cast<const floatx4*>(row + off);
+  const floatx4 hi = *reinterpret_cast<const floatx4*>(row + off + 8);
+  Frag<float> f;
+  f.v[0] = lo[0]; f.v[1] = lo[1]; f.v[2] = lo[2]; f.v[3] = lo[3];
+  f.v[4] = hi[0]; f.v[5] = hi[1]; f.v[6] = hi[2]; f.v[7] = hi[3];
+  return f;
+}
+
+// out(32x32) += X^T B' with X a 32x32 accumulator tile and B'[a][j] = src[j*ld + a].
+template <typename T>
+__device__ __forceinline__ void mma_xt(floatx16& out, const floatx16& X, const T* src, int ld) {
+  const T* row = src + (lane_id() & 31) * ld;
+  mma(out, frag_from_acc<T>(X, 0), ld_frag_perm(row, 0));
+  mma(out, frag_from_acc<T>(X, 1), ld_frag_perm(row, 1));
+}
+
+// Compile-time K version of mma_tile (fully unrolled; lda / ldb are usually
+// compile-time too, so the LDS offsets become immediates).
+template <typename T, int K>
+__device__ __forceinline__ void mma_k(floatx16& acc, const T* a, int lda, const T* b, int ldb) {
+  const int lane = lane_id();
+  const T* ap = a + (lane & 31) * lda + (lane >> 5) * 8;
+  const T* bp = b + (lane & 31) * ldb + (lane >> 5) * 8;
+#pragma unroll
+  for (int k = 0; k < K / 16; ++k) mma(acc, ld_frag(ap + 16 * k), ld_frag(bp + 16 * k));
+}
+
+// The two A fragments of an accumulator tile (see frag_from_acc), converted once.
+template <typename T> struct AccFrags { Frag<T> f[2]; };
+template <typename T>
+__device__ __forceinline__ AccFrags<T> acc_frags(const floatx16& x) {
+  AccFrags<T> a;
+  a.f[0] = frag_from_acc<T>(x, 0);
+  a.f[1] = frag_from_acc<T>(x, 1);
+  return a;
+}
+// out(32x32) += X^T B' with X given by its converted fragments, B'[a][j] = src[j*ld + a].
+template <typename T>
+__device__ __forceinline__ void mma_xt_f(floatx16& out, const AccFrags<T>& X, const T* src, int ld) {
+  const T* row = src + (lane_id() & 31) * ld;
+  mma(out, X.f[0], ld_frag_perm(row, 0));
+  mma(out, X.f[1], ld_frag_perm(row, 1));
+}
+
+// The 16 per-register row values base[row(v)] of this lane (rows 8r + 4*(lane/32) + q),
+// read as four 16-byte LDS loads (base 16-byte aligned).
+__device__ __forceinline__ void rows16(const float* base, float (&o)[16]) {
+  const float* p = base + 4 * (lane_id() >> 5);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(p + 8 * r);
+    o[4 * r + 0] = v[0]; o[4 * r + 1] = v[1]; o[4 * r + 2] = v[2]; o[4 * r + 3] = v[3];
+  }
+}
+
 // Sum over the 32 columns of each row: after the call every lane holds, for
 // each of its 16 registers, the full row sum (lanes of one 32-lane half agree).
 __device__ __forceinline__ float row_reduce32(float v) {
@@ -124,6 +216,163 @@ __host__ __device__ __forceinline__ int round_up(int x, int m) { return (x + m -
 // LDS row pitch (elements) for a k-contiguous tile of width w: +16 bytes so
 // consecutive rows start in different banks.
 template <typename T> __host__ __device__ constexpr int lds_pitch(int w) { return w + 16 / (int)sizeof(T); }
+
+// ---------------------------------------------------------------------------
+// Global -> LDS staging of a 64-row block of a row-major (rows, features)
+// tensor: rows row0 + [r0, r0 + 64) (valid below `len`), features
+// [col0, col0 + width) of a row of `ld` elements, zero-filled up to `wpad`.
+// `vec_ok` (uniform) says 16-byte loads are aligned (width, ld, col0 multiples
+// of 16/sizeof(T) and a 16-byte aligned base); otherwise scalar loads.
+// ---------------------------------------------------------------------------
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct Vec16<float> { typedef floatx4 type; static constexpr int n = 4; };
+
+// natural layout: out[r][k] (pitch elements per row)
+template <typename T>
+__device__ __forceinline__ void stage_nat(T* __restrict__ out, int pitch, const T* __restrict__ src, int64_t ld,
+                                          int64_t col0, int64_t row0, int r0, int len, int width, int wpad,
+                                          bool vec_ok) {
+  constexpr int V = Vec16<T>::n;
+  typedef typename Vec16<T>::type VT;
+  const int per_row = wpad / V;
+  const int total = SSD_BLK * per_row;
+  for (int id = threadIdx.x; id < total; id += blockDim.x) {
+    const int r = id / per_row, k = (id - r * per_row) * V;
+    const bool rv = r0 + r < len;
+    const T* g = src + (row0 + r0 + r) * ld + col0 + k;
+    VT v;
+    if (vec_ok) {
+      if (rv && k < width) v = *reinterpret_cast<const VT*>(g);
+      else for (int e = 0; e < V; ++e) v[e] = from_f<T>(0.0f);
+    } else {
+      for (int e = 0; e < V; ++e) v[e] = (rv && k + e < width) ? g[e] : from_f<T>(0.0f);
+    }
+    *reinterpret_cast<VT*>(out + r * pitch + k) = v;
+  }
+}
+
+// transposed layout: out[k][r]; lanes of a wave take consecutive rows so the
+// 2-byte LDS stores of one feature land in consecutive banks.
+template <typename T>
+__device__ __forceinline__ void stage_tr(T* __restrict__ out, int pitch, const T* __restrict__ src, int64_t ld,
+                                         int64_t col0, int64_t row0, int r0, int len, int width, int wpad,
+                                         bool vec_ok) {
+  constexpr int V = Vec16<T>::n;
+  typedef typename Vec16<T>::type VT;
+  const int total = SSD_BLK * (wpad / V);
+  for (int id = threadIdx.x; id < total; id += blockDim.x) {
+    const int r = id & (SSD_BLK - 1), k = (id >> 6) * V;
+    const bool rv = r0 + r < len;
+    const T* g = src + (row0 + r0 + r) * ld + col0 + k;
+    VT v;
+    if (vec_ok) {
+      if (rv && k < width) v = *reinterpret_cast<const VT*>(g);
+      else for (int e = 0; e < V; ++e) v[e] = from_f<T>(0.0f);
+    } else {
+      for (int e = 0; e < V; ++e) v[e] = (rv && k + e < width) ? g[e] : from_f<T>(0.0f);
+    }
+    for (int e = 0; e < V; ++e) out[(k + e) * pitch + r] = v[e];
+  }
+}
+
+// transposed layout with every row scaled by scale[r] (fp32) before rounding.
+template <typename T>
+__device__ __forceinline__ void stage_tr_scaled(T* __restrict__ out, int pitch, const T* __restrict__ src,
+                                                int64_t ld, int64_t col0, int64_t row0, int r0, int len, int width,
+                                                int wpad, bool vec_ok, const float* __restrict__ scale) {
+  constexpr int V = Vec16<T>::n;
+  typedef typename Vec16<T>::type VT;
+  const int total = SSD_BLK * (wpad / V);
+  for (int id = threadIdx.x; id < total; id += blockDim.x) {
+    const int r = id & (SSD_BLK - 1), k = (id >> 6) * V;
+    const bool rv = r0 + r < len;
+    const T* g = src + (row0 + r0 + r) * ld + col0 + k;
+    VT v;
+    if (vec_ok) {
+      if (rv && k < width) v = *reinterpret_cast<const VT*>(g);
+      else for (int e = 0; e < V; ++e) v[e] = from_f<T>(0.0f);
+    } else {
+      for (int e = 0; e < V; ++e) v[e] = (rv && k + e < width) ? g[e] : from_f<T>(0.0f);
+    }
+    const float sc = rv ? scale[r] : 0.0f;
+    for (int e = 0; e < V; ++e) out[(k + e) * pitch + r] = from_f<T>(to_f(v[e]) * sc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register-staged tiles: a 64-row x wpad (<= 128) block is loaded by the 256
+// threads of a block into registers first (all loads in flight together), then
+// written to LDS in natural and/or transposed layout. Element (r, k) of the
+// tile belongs to vector id = r + 64 * (k / V) (TR mapping: the 64 lanes of a
+// wave hold 64 consecutive rows, so transposed 2-byte stores hit consecutive
+// banks) or id = r * (wpad / V) + k / V (row-major mapping: a wave reads whole
+// rows, fully coalesced). Thread t owns ids t, t + 256, ...
+// ---------------------------------------------------------------------------
+template <typename T, int MAXW = 128> struct TileRegs {
+  static constexpr int V = Vec16<T>::n;
+  static constexpr int MAXQ = SSD_BLK * MAXW / V / 256;  // vectors per thread for wpad = MAXW
+  typename Vec16<T>::type v[MAXQ];
+};
+
+template <typename T, bool TRMAP, int MAXW>
+__device__ __forceinline__ void tile_load(TileRegs<T, MAXW>& t, const T* __restrict__ src, int64_t ld, int64_t col0,
+                                          int64_t row0, int r0, int len, int width, int wpad, bool vec_ok) {
+  constexpr int V = Vec16<T>::n;
+  const int per_row = wpad / V, total = SSD_BLK * per_row;
+#pragma unroll
+  for (int q = 0; q < TileRegs<T, MAXW>::MAXQ; ++q) {
+    const int id = threadIdx.x + q * 256;
+    if (id < total) {
+      const int r = TRMAP ? (id & (SSD_BLK - 1)) : id / per_row;
+      const int k = TRMAP ? (id >> 6) * V : (id - r * per_row) * V;
+      const bool rv = r0 + r < len;
+      const T* g = src + (row0 + r0 + r) * ld + col0 + k;
+      if (vec_ok) {
+        if (rv && k < width) t.v[q] = *reinterpret_cast<const typename Vec16<T>::type*>(g);
+        else for (int e = 0; e < V; ++e) t.v[q][e] = from_f<T>(0.0f);
+      } else {
+        for (int e = 0; e < V; ++e) t.v[q][e] = (rv && k + e < width) ? g[e] : from_f<T>(0.0f);
+      }
+    }
+  }
+}
+
+template <typename T, bool TRMAP, int MAXW>
+__device__ __forceinline__ void tile_store_nat(const TileRegs<T, MAXW>& t, T* __restrict__ out, int pitch, int wpad) {
+  constexpr int V = Vec16<T>::n;
+  const int per_row = wpad / V, total = SSD_BLK * per_row;
+#pragma unroll
+  for (int q = 0; q < TileRegs<T, MAXW>::MAXQ; ++q) {
+    const int id = threadIdx.x + q * 256;
+    if (id < total) {
+      const int r = TRMAP ? (id & (SSD_BLK - 1)) : id / per_row;
+      const int k = TRMAP ? (id >> 6) * V : (id - r * per_row) * V;
+      *reinterpret_cast<typename Vec16<T>::type*>(out + r * pitch + k) = t.v[q];
+    }
+  }
+}
+
+// transposed: out[k][r]; rows scaled by scale[r] when scale != nullptr
+template <typename T, int MAXW>
+__device__ __forceinline__ void tile_store_tr(const TileRegs<T, MAXW>& t, T* __restrict__ out, int pitch, int wpad,
+                                              const float* __restrict__ scale = nullptr) {
+  constexpr int V = Vec16<T>::n;
+  const int total = SSD_BLK * (wpad / V);
+#pragma unroll
+  for (int q = 0; q < TileRegs<T, MAXW>::MAXQ; ++q) {
+    const int id = threadIdx.x + q * 256;
+    if (id < total) {
+      const int r = id & (SSD_BLK - 1), k = (id >> 6) * V;
+      if (scale) {
+        const float sc = scale[r];
+        for (int e = 0; e < V; ++e) out[(k + e) * pitch + r] = from_f<T>(to_f(t.v[q][e]) * sc);
+      } else {
+        for (int e = 0; e < V; ++e) out[(k + e) * pitch + r] = t.v[q][e];
+      }
+    }
+  }
+}
 
 // One entry of the chunk table: chunk k of sequence `seq` covers rows
 // [row0, row0 + len) of the packed token axis; `first` marks k == 0.

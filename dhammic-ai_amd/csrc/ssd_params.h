@@ -6,16 +6,17 @@
 
 #include "ssd_common.h"
 
-// Rows of the token axis per block tile inside a chunk.
-#define SSD_BLK 64
 
 struct SsdDims {
   int batch, seqlen, H, P, G, N, Q;  // Q: tokens per chunk
-  int Ppad, Npad, Qpad;              // P, N rounded up to 32; Q rounded up to 64
+  int Ppad, Npad, Qpad;              // P, N padded to 32, 64 or 128; Q rounded up to 64
   int nseq, max_chunks, hpg;         // hpg: heads per group
   int64_t R;                         // rows of the packed token axis (batch * seqlen)
   int a_mode, has_dt, has_D, has_z, has_init, has_dfinal, varlen;
   float eps;
+  // 16-byte global loads allowed for x/dy/z-shaped tensors and for B/C (set per call
+  // from the feature widths and the pointers' alignment)
+  bool vec_x, vec_bc;
 };
 
 // Internal buffers (all inside the caller's workspaces).

@@ -47,19 +47,8 @@ __global__ void __launch_bounds__(256) k_chunk_state(SsdDims d, const ChunkInfo*
   const int64_t urow = (int64_t)d.H * d.P, vrow = (int64_t)d.G * d.N;
   for (int kb = 0; kb < ci.len; kb += SSD_BLK) {
     __syncthreads();
-    for (int idx = threadIdx.x; idx < SSD_BLK * d.Ppad; idx += blockDim.x) {
-      const int l = idx / d.Ppad, p = idx % d.Ppad;
-      float v = 0.0f;
-      if (kb + l < ci.len && p < d.P) v = to_f(U[(int64_t)(ci.row0 + kb + l) * urow + (int64_t)h * d.P + p]);
-      UT[p * KP + l] = from_f<T>(v);
-    }
-    for (int idx = threadIdx.x; idx < SSD_BLK * d.Npad; idx += blockDim.x) {
-      const int l = idx / d.Npad, n = idx % d.Npad;
-      float v = 0.0f;
-      if (kb + l < ci.len && n < d.N)
-        v = coef[kb + l] * to_f(V[(int64_t)(ci.row0 + kb + l) * vrow + (int64_t)g * d.N + n]);
-      VT[n * KP + l] = from_f<T>(v);
-    }
+    stage_tr<T>(UT, KP, U, urow, (int64_t)h * d.P, ci.row0, kb, ci.len, d.P, d.Ppad, d.vec_x);
+    stage_tr_scaled<T>(VT, KP, V, vrow, (int64_t)g * d.N, ci.row0, kb, ci.len, d.N, d.Npad, d.vec_bc, coef + kb);
     __syncthreads();
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {

@@ -101,7 +101,7 @@ def test_validation_accepts_benchmark_configs(capi):
     (dict(chunk=512), "SSD_ERR_UNSUPPORTED"),
     (dict(headdim=256), "SSD_ERR_UNSUPPORTED"),
     (dict(dstate=160), "SSD_ERR_UNSUPPORTED"),
-    (dict(dtype=0), "SSD_ERR_UNSUPPORTED"),                      # fp32 tiles exceed LDS at N=128, P=64
+    (dict(dtype=0, headdim=128), "SSD_ERR_UNSUPPORTED"),         # fp32 tiles exceed LDS at N=128, P=128
 ])
 def test_validation_rejects(capi, kw, status):
     assert _validate(capi, **kw) == getattr(capi, status)
