@@ -2,7 +2,7 @@
 """SSD scan fwd+bwd throughput on one MI355X, with the dominant kernel's
 roofline and the reference CPU path timed on the host beside it.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--copy-probe]
 
 A step is one forward + backward of the fused chunked SSD scan over the
 1.3B-class layer: B=4, L=8192, H=64, P=64, G=1, N=128,
@@ -84,12 +84,43 @@ def phase_models(nchunks):
     return m
 
 
-def time_gpu(steps, warmup):
+COPY_PROBE_BYTES = 1 << 30
+
+
+def copy_probe(dev):
+    """One plain device copy of COPY_PROBE_BYTES (read once, written once):
+    the calibration dispatch for the FETCH_SIZE / WRITE_SIZE counter runs."""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel`, from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-probe factor), or None."""
+    import re
+    f = ROOT / "profiles" / "ssd_config2_hbm_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        m = re.match(r"^- traffic (\w+): (\d+) bytes", line)
+        if m and m.group(1) == kernel:
+            return int(m.group(2))
+    return None
+
+
+def time_gpu(steps, warmup, probe=False):
     import torch
     from kernels import _capi as C_
     from kernels import ssd_scan as S
 
     dev = torch.device("cuda", 0)
+    if probe:
+        copy_probe(dev)
     t = make_inputs(dev)
     cfg = S._Cfg(chunk=CFG["chunk"], a_mode=C_.SSD_A_PER_HEAD, nseq=CFG["batch"], varlen=False,
                  state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=1e-6)
@@ -159,7 +190,7 @@ def roofline(phases, nchunks):
     out["kernel_ms"] = phases[name]
     out["algorithmic_flops"] = flops
     out["algorithmic_bytes"] = nbytes
-    out["traffic"] = None
+    out["traffic"] = measured_traffic(name)
     return out
 
 
@@ -214,6 +245,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run one plain 1 GiB device copy first (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); the SSD scan is sharded "
@@ -221,7 +254,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
-    ms_step, wall_ms, phases, nchunks = time_gpu(a.steps, a.warmup)
+    ms_step, wall_ms, phases, nchunks = time_gpu(a.steps, a.warmup, a.copy_probe)
     tokens = CFG["batch"] * CFG["seqlen"]
     value = tokens / (ms_step * 1e-3) / 1e6
     rl = roofline(phases, nchunks)

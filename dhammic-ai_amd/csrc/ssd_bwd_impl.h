@@ -207,6 +207,7 @@ __global__ void __launch_bounds__(256) k_bwd_col(SsdDims d, SsdBufs bf, BwdCommo
     __syncthreads();
     float* colG = bf.colG + ((int64_t)c * d.H + h) * d.Qpad;
     if (threadIdx.x < SSD_BLK) colG[s0 + threadIdx.x] = red[threadIdx.x] + red[SSD_BLK + threadIdx.x];
+    __syncthreads();  // the gcol partials are read before the e / xs partials overwrite them
     const float cs_last = s_cs[d.Qpad - 1];
     float dpart = 0.0f;
     const float Dh = d.has_D ? in.Dv[h] : 0.0f;

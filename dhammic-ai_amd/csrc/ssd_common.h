@@ -199,6 +199,30 @@ __device__ __forceinline__ void rows16(const float* base, float (&o)[16]) {
   }
 }
 
+// One MFMA operand fragment (8 consecutive features k .. k+7 of row `row`)
+// read straight from a row-major global tensor, zero outside the row range /
+// feature width. vec_ok: 16-byte loads are aligned (see stage_nat).
+template <typename T>
+__device__ __forceinline__ Frag<T> frag_global(const T* __restrict__ src, int64_t ld, int64_t col0, int64_t row,
+                                               bool row_ok, int k, int width, bool vec_ok) {
+  Frag<T> f;
+  const T* g = src + row * ld + col0 + k;
+  if (vec_ok && row_ok && k + 8 <= width) {
+    if constexpr (sizeof(T) == 2) {
+      f.v = *reinterpret_cast<const bf16x8*>(g);
+    } else {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(g);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(g + 4);
+      f.v[0] = a[0]; f.v[1] = a[1]; f.v[2] = a[2]; f.v[3] = a[3];
+      f.v[4] = b[0]; f.v[5] = b[1]; f.v[6] = b[2]; f.v[7] = b[3];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = (row_ok && k + e < width) ? g[e] : from_f<T>(0.0f);
+  }
+  return f;
+}
+
 // Sum over the 32 columns of each row: after the call every lane holds, for
 // each of its 16 registers, the full row sum (lanes of one 32-lane half agree).
 __device__ __forceinline__ float row_reduce32(float v) {

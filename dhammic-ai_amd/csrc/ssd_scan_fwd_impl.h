@@ -22,7 +22,7 @@
 // B and x rows of block j+1 are loaded into registers while block j computes.
 // ---------------------------------------------------------------------------
 template <typename T, int HS, int PT, int NT>
-__global__ void __launch_bounds__(256) k_chunk_scan_fwd(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_chunk_scan_fwd(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                         const float* __restrict__ cs, const T* __restrict__ hin,
                                                         const T* __restrict__ x, const float* __restrict__ dt,
                                                         const T* __restrict__ Bm, const T* __restrict__ Cm,
@@ -148,12 +148,13 @@ inline size_t lds_scan_fwd_hs(size_t es, const SsdDims& d, size_t hs) {
   return 2 * sizeof(float) * hs * d.Qpad + es * (2 * SSD_BLK * NP + hs * d.Ppad * BP);
 }
 
-// Heads per block: the largest of 4, 2, 1 that divides the heads of a group
-// and fits the LDS budget (all heads of a block read the same B and C).
+// Heads per block: 2 when the heads of a group allow it and two blocks then fit
+// one CU's LDS (80 KiB each), else 1. All heads of a block share B and C; two
+// heads keep the register count low enough for two blocks per CU, whose
+// interleaving hides the barrier and load latency of each.
 inline int fwd_heads_per_block(int dtype, const SsdDims& d) {
   const size_t es = dtype == 1 ? 2 : 4;
-  for (int hs = 4; hs > 1; hs >>= 1)
-    if (d.hpg % hs == 0 && lds_scan_fwd_hs(es, d, hs) <= 128 * 1024) return hs;
+  if (d.hpg % 2 == 0 && lds_scan_fwd_hs(es, d, 2) <= 80 * 1024) return 2;
   return 1;
 }
 
@@ -190,7 +191,6 @@ hipError_t scan_fwd_p(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void*
 template <typename T>
 hipError_t scan_fwd_dispatch(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
   const int hs = fwd_heads_per_block(sizeof(T) == 2 ? 1 : 0, d);
-  if (hs == 4) return scan_fwd_p<T, 4>(d, b, in, y, s);
   if (hs == 2) return scan_fwd_p<T, 2>(d, b, in, y, s);
   return scan_fwd_p<T, 1>(d, b, in, y, s);
 }
