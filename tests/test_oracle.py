@@ -296,12 +296,53 @@ def test_extended_varlen_equals_batched():
     assert (fb - fs).abs().max().item() < 1e-7
 
 
-def test_extended_gated_norm_closed_form():
+def test_extended_gated_norm_invariants():
+    """Properties that fix the norm: scale invariance (eps = 0), unit RMS of the
+    normalised row (w = 1, gate divided out), eps inside the square root (a
+    constant row c gives c / sqrt(c^2 + eps)), reduction over the last dim only."""
+    from oracle.ssd_extended import gated_rmsnorm
     g = torch.Generator().manual_seed(5)
     y = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
     z = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
     w = torch.randn(8, generator=g, dtype=torch.float64)
+    assert torch.allclose(gated_rmsnorm(3.7 * y, z, w, 0.0), gated_rmsnorm(y, z, w, 0.0), atol=1e-13)
+    gate = torch.nn.functional.silu(z)
+    u = gated_rmsnorm(y, z, torch.ones(8, dtype=torch.float64), 0.0) / gate
+    assert torch.allclose(u.pow(2).mean(-1), torch.ones(2, 3, dtype=torch.float64), atol=1e-12)
+    c, eps = 0.05, 1e-3
+    row = torch.full((1, 1, 8), c, dtype=torch.float64)
+    one = torch.ones(8, dtype=torch.float64)
+    out = gated_rmsnorm(row, torch.full_like(row, 50.0), one, eps)  # silu(50) = 50 to 1e-20
+    assert torch.allclose(out, torch.full_like(row, c / math.sqrt(c * c + eps) * 50.0), rtol=1e-12)
+    # rows are independent: changing one row leaves the others unchanged
+    y2 = y.clone()
+    y2[0, 0] *= -5.0
+    assert torch.equal(gated_rmsnorm(y2, z, w, 1e-6)[1], gated_rmsnorm(y, z, w, 1e-6)[1])
+
+
+def test_extended_gated_norm_backward_matches_reference_closed_form():
+    """The reference documents RMSNorm's backward in closed form
+    (r2/dhammic-ai/src/kernels/rmsnorm.py:15-36): with r = rsqrt(mean(x^2) + e),
+    s = sum_j w_j x_j g_j, dx_i = r (w_i g_i - (x_i / D) r^2 s), dw = sum_rows x r g.
+    The oracle differentiates by autograd; composing the closed form with the
+    gate's product rule must give the same gradients."""
     from oracle.ssd_extended import gated_rmsnorm
-    out = gated_rmsnorm(y, z, w, 1e-6)
-    ref = y / torch.sqrt((y * y).mean(-1, keepdim=True) + 1e-6) * w * (z / (1 + torch.exp(-z)))
-    assert torch.allclose(out, ref, atol=1e-14)
+    g = torch.Generator().manual_seed(6)
+    D, eps = 16, 1e-6
+    y = torch.randn(5, D, generator=g, dtype=torch.float64, requires_grad=True)
+    z = torch.randn(5, D, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(D, generator=g, dtype=torch.float64, requires_grad=True)
+    go = torch.randn(5, D, generator=g, dtype=torch.float64)
+    dy, dz, dw = torch.autograd.grad(gated_rmsnorm(y, z, w, eps), (y, z, w), go)
+    with torch.no_grad():
+        sig = torch.sigmoid(z)
+        gate = z * sig
+        r = torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + eps)
+        gn = go * gate                                   # gradient reaching the norm's output
+        s = (w * y * gn).sum(-1, keepdim=True)
+        dy_ref = r * (w * gn - (y / D) * r * r * s)
+        dw_ref = (y * r * gn).sum(0)
+        dz_ref = go * (y * r * w) * (sig * (1 + z * (1 - sig)))
+    assert torch.allclose(dy, dy_ref, atol=1e-12)
+    assert torch.allclose(dw, dw_ref, atol=1e-12)
+    assert torch.allclose(dz, dz_ref, atol=1e-12)
