@@ -45,7 +45,12 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
     const int l = lane * per + e;
     float x = 0.0f;
     if (l < ci.len) {
-      x = bf.rowG[base + l] - bf.colG[base + l] + bf.dcs_off[base + l] - bf.eterm[base + l];
+      // rowG partial k covers the rows of blocks >= k (column set k of the fused
+      // path starts at column block k); the column / row path writes one partial
+      float rg = 0.0f;
+      for (int k = 0; k < bf.nrowg && k <= l / 64; ++k)
+        rg += bf.rowG[(int64_t)k * d.max_chunks * d.H * d.Qpad + base + l];
+      x = rg - bf.colG[base + l] + bf.dcs_off[base + l] - bf.eterm[base + l];
       esum += bf.eterm[base + l];
     }
     v[e] = x;

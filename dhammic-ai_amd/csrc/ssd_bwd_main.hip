@@ -1,0 +1,640 @@
+// Fused backward of the chunked SSD scan for bf16 inputs (gfx950), the work
+// that FusedSSDScan.backward (r2/dhammic-ai/src/kernels/ssd_scan.py:467-533)
+// gets by re-running the forward under autograd, written out per chunk.
+//
+// Notation per (chunk, head h); rows l (outputs) and columns s (inputs) of the
+// chunk's 64-token blocks, tile (i, j) = rows of block i x columns of block j:
+//   S = C B^T (shared by the heads of a group), L[l,s] = exp(clamp(cs_l - cs_s)),
+//   M = S*L, dM[l,s] = dy_l . x_s, dm = dM dt_s, G = dm*M*pass(cs_l - cs_s)
+// gives per head
+//   dX_s   = sum_l M[l,s] dy_l + w_s B_s dst^T           (dx = dt dX + D dy)
+//   rowG_l = sum_s G[l,s],  colG_s = sum_l G[l,s]
+//   E_s    = pass_w(s) dt_s x_s . (w_s B_s dst^T),  xdx_s = x_s . dX_s
+//   dcs_off_l = pass(cs_l) C_l . (exp(cs_l) dy_l h_in)
+// and, summed over the heads of the group,
+//   dS[l,s] = sum_h dm L                   (-> dB = dS^T C, dC = dS B, kernel k_bwd_bc)
+//   dBs_s   = sum_h w_s dt_s x_s dst       (state part of dB)
+//   dCo_l   = sum_h exp(cs_l) dy_l h_in    (Y_off part of dC)
+//
+// k_bwd_main: one block per (column block j, chunk, group, head slice). The
+// block owns the 64 columns s of block j, so dX, colG and the state part of dB
+// are complete there; it walks the tiles (i, j), i >= j, of every head of its
+// slice. S for those tiles is computed once per block and kept in registers;
+// dS accumulates in registers over the slice's heads. Tiles are computed
+// transposed ([s rows][l lanes]): row sums of G are per-lane, column sums are
+// reduced across lanes once per head. M goes through a per-wave LDS tile to
+// become the B operand of dX^T = dY^T M; every other operand is read from
+// natural-layout LDS tiles (ds_read_b64_tr_b16 where the contraction runs over
+// the row index).
+#include "ssd_launch.h"
+#include "ssd_tile.h"
+
+struct BwdMainArgs {
+  const ChunkInfo* chunks;
+  const float* cs;    // [MC][H][Qpad]
+  const bf16* hin;    // [MC][H][Ppad][Npad]
+  const float* dst;   // [MC][H][Ppad][Npad]
+  const bf16* x;
+  const float* dt;
+  const bf16* Bm;
+  const bf16* Cm;
+  const float* Dv;
+  const bf16* dy;
+  bf16* dx;
+  float* rowG;        // [nb][MC][H][Qpad], partial per column block (block j covers rows >= 64 j)
+  float* colG;        // [MC][H][Qpad]
+  float* eterm;
+  float* xdx;
+  float* dcs_off;
+  float* dD_part;     // [MC][H][Qpad/64]
+  float* dS;          // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
+  float* dBs;         // [nslices][R][G][N]
+  float* dCo;         // [nslices][R][G][N]
+  int nslices, hslice;
+};
+
+constexpr int kMaxSlots = 4;  // tiles per column block (nb <= 4)
+
+template <int PT, int NT>
+struct BwdMainLds {
+  static constexpr int PP = 32 * PT, NP = 32 * NT;
+  static constexpr int RED = 1024;  // floats of reduction scratch
+  static size_t bytes(int Qpad) {
+    const size_t xch = 2 * PT * 4096;
+    return sizeof(float) * (2 * Qpad + RED) + 2 * (size_t)(64 * PP + 4 * 64 * PP + 2 * PP * NP + 64 * NP + 4 * 1024) +
+           xch;
+  }
+};
+
+// One block per (column block j, group, head slice, chunk); blocks are
+// numbered column-major with the heaviest column (j = 0, nb tiles) first, and
+// the column blocks of one chunk share an XCD (same block index mod 8).
+template <int PT, int NT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_bwd_main(SsdDims d, BwdMainArgs a) {
+  constexpr int PP = 32 * PT, NP = 32 * NT;
+  constexpr int NTW = (NT + 1) / 2;  // n tiles per wave in the state terms
+  constexpr int PTW = (PT + 1) / 2;  // p tiles kept per wave after the dX exchange
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = d.Qpad / 64;
+
+  const int U = d.max_chunks * d.G * a.nslices;
+  const int U8 = (U + 7) / 8 * 8;
+  const int j = blockIdx.x / U8;
+  const int u = blockIdx.x % U8;
+  if (u >= U) return;
+  const int c = u % d.max_chunks;
+  const int gsl = u / d.max_chunks;
+  const int g = gsl / a.nslices, slc = gsl % a.nslices;
+  const ChunkInfo ci = a.chunks[c];
+  const int nbl = (ci.len + 63) >> 6;
+  if (j >= nbl) return;
+  const int nt_i = nbl - j;  // tiles (i, j), i = j .. nbl-1
+  const int h_lo = g * d.hpg + slc * a.hslice;
+  const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
+  if (h_lo >= h_hi) return;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w & 1, wc = w >> 1;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int Qpad = d.Qpad;
+  const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
+
+  float* s_cs2 = reinterpret_cast<float*>(smem);  // cs * log2(e) of the current head
+  float* s_dt = s_cs2 + Qpad;
+  float* red = s_dt + Qpad;                        // RED floats
+  float* red_row = red;                            // [4 blocks][2 wr][64]
+  float* red_col = red + 512;                      // [2 wc][64]
+  float* red_e = red + 640;                        // [2 wc][64]
+  float* red_x = red + 768;                        // [2 wc][64]
+  float* red_o = red + 896;                        // [2 wc][64] (the first 4 also hold the dD partials)
+  bf16* xj = reinterpret_cast<bf16*>(red + BwdMainLds<PT, NT>::RED);  // [64][PP]
+  bf16* dYt = xj + 64 * PP;                        // [4][64][PP] (blocks j .. nbl-1 used)
+  bf16* dstT = dYt + 4 * 64 * PP;                  // [PP][NP]
+  bf16* hinT = dstT + PP * NP;                     // [PP][NP]
+  bf16* Bt = hinT + PP * NP;                       // [64][NP]
+  bf16* Mb = Bt + 64 * NP + w * 1024;              // this wave's [32][32]
+  float* xch = reinterpret_cast<float*>(Bt + 64 * NP + 4 * 1024);
+
+  // ---- B tile of column block j ----
+  {
+    TileStage<64, NP, 256> st;
+    tstage_load(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
+                min(64, ci.len - 64 * j), d.N, d.vec_bc);
+    tstage_store(st, Bt);
+  }
+  __syncthreads();
+
+  // ---- S^T tiles (i, j), slot t = i - j: rows s (wr half of block j), lanes l (wc half of block i) ----
+  bf16x8 S[kMaxSlots][2];  // kept in bf16: M = S L is rounded to bf16 for the MFMA anyway
+  floatx16 dS[kMaxSlots];
+#pragma unroll
+  for (int t = 0; t < kMaxSlots; ++t) {
+    floatx16 sacc;
+    zero(sacc);
+    zero(dS[t]);
+    S[t][0] = acc_frag(sacc, 0);
+    S[t][1] = acc_frag(sacc, 1);
+    if (t >= nt_i) continue;
+    const int i = j + t;
+    if (t == 0 && wr == 1 && wc == 0) continue;  // above the diagonal
+    const int lrow = 64 * i + 32 * wc + l32;
+    const bool lok = lrow < ci.len;
+    const bf16* crow = a.Cm + (int64_t)(ci.row0 + (lok ? lrow : 0)) * brow + (int64_t)g * d.N;
+#pragma unroll
+    for (int kk = 0; kk < NP; kk += 16) {
+      const int n0 = kk + 8 * hh;
+      bf16x8 cb;
+      if (lok && d.vec_bc && n0 < d.N) {
+        cb = *reinterpret_cast<const bf16x8*>(crow + n0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cb[e] = (lok && n0 + e < d.N) ? crow[n0 + e] : (bf16)0.0f;
+      }
+      mfma(sacc, tld8<NP>(Bt, 32 * wr + l32, n0), cb);
+    }
+    S[t][0] = acc_frag(sacc, 0);
+    S[t][1] = acc_frag(sacc, 1);
+  }
+
+  // per-token lane of the state terms: token 32 wr + l32 of block j, n tiles nt = 2 ntk + wc
+  const int t_loc = 32 * wr + l32;
+  const int tg = 64 * j + t_loc;
+  const bool t_ok = tg < ci.len;
+  floatx16 dBT[NTW], dCoT[NTW];
+#pragma unroll
+  for (int ntk = 0; ntk < NTW; ++ntk) {
+    zero(dBT[ntk]);
+    zero(dCoT[ntk]);
+  }
+
+  for (int h = h_lo; h < h_hi; ++h) {
+    __syncthreads();  // the previous head's LDS reads are done
+    {
+      const float* csc = a.cs + ((int64_t)c * d.H + h) * Qpad;
+      for (int l = threadIdx.x; l < Qpad; l += 256) {
+        s_cs2[l] = csc[l] * SSD_LOG2E;
+        s_dt[l] = (d.has_dt && l < ci.len) ? a.dt[(int64_t)(ci.row0 + l) * d.H + h] : 1.0f;
+      }
+      for (int e = threadIdx.x; e < 4 * 2 * 64; e += 256) red_row[e] = 0.0f;
+      TileStage<64, PP, 256> sx;
+      tstage_load(sx, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + (int64_t)h * d.P, xrow,
+                  min(64, ci.len - 64 * j), d.P, d.vec_x);
+      TileStage<PP, NP, 256> sd, sh;
+      tstage_load_f32(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP);
+      tstage_load(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP, true);
+      for (int i = j; i < nbl; ++i) {
+        TileStage<64, PP, 256> st;
+        tstage_load(st, a.dy + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
+                    min(64, ci.len - 64 * i), d.P, d.vec_x);
+        tstage_store(st, dYt + i * 64 * PP);
+      }
+      tstage_store(sx, xj);
+      tstage_store(sd, dstT);
+      tstage_store(sh, hinT);
+    }
+    __syncthreads();
+
+    const float cs_last = s_cs2[Qpad - 1];
+    const float Dh = d.has_D ? a.Dv[h] : 0.0f;
+
+    float colacc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) colacc[v] = 0.0f;
+    floatx16 dXT[PT];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) zero(dXT[pt]);
+
+#pragma unroll
+    for (int t = 0; t < kMaxSlots; ++t) {
+      if (t >= nt_i) continue;
+      const int i = j + t;
+      const bool diag = t == 0;
+      if (diag && wr == 1 && wc == 0) continue;
+      const bf16* dyi = dYt + i * 64 * PP;
+      floatx16 dm;
+      zero(dm);
+#pragma unroll
+      for (int kk = 0; kk < PP; kk += 16)
+        mfma(dm, tld8<PP>(xj, 32 * wr + l32, kk + 8 * hh), tld8<PP>(dyi, 32 * wc + l32, kk + 8 * hh));
+      const int l_loc = 32 * wc + l32;
+      const float cs_l = s_cs2[64 * i + l_loc];
+      float cs_s[16], dt_s[16];
+      rows16(s_cs2 + 64 * j + 32 * wr, cs_s);
+      rows16(s_dt + 64 * j + 32 * wr, dt_s);
+      float rsum = 0.0f;
+      float Mv[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int s_loc = 32 * wr + acc_row(v, lane);
+        const float dd = cs_l - cs_s[v];
+        float Lv = exp2_fast(clamp_med3(dd, -SSD_T2, SSD_T2));
+        if (diag && s_loc > l_loc) Lv = 0.0f;
+        const float dmv = dm[v] * dt_s[v];
+        const float M = (float)S[t][v >> 3][v & 7] * Lv;
+        dS[t][v] = fmaf(dmv, Lv, dS[t][v]);
+        const float Mp = fabsf(dd) < SSD_T2 ? M : 0.0f;
+        const float gg = dmv * Mp;
+        colacc[v] += gg;
+        rsum += gg;
+        Mv[v] = M;
+      }
+      // M^T (rows s, lanes l) -> this wave's LDS tile Mb[l][s]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bf16x4 q;
+        q[0] = (bf16)Mv[4 * r + 0];
+        q[1] = (bf16)Mv[4 * r + 1];
+        q[2] = (bf16)Mv[4 * r + 2];
+        q[3] = (bf16)Mv[4 * r + 3];
+        *reinterpret_cast<bf16x4*>(Mb + toff<32>(l32, 8 * r + 4 * hh)) = q;
+      }
+      // dX^T[p][s] += sum_l dy_i[l][p] M[l][s]  (l over this wave's 32-row window)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8 mb = ttr_std<32>(Mb, 16 * kk, 0);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) mfma(dXT[pt], ttr_std<PP>(dyi, 32 * wc + 16 * kk, 32 * pt), mb);
+      }
+      // row sums of G: per lane over its 16 s rows, then the two half-waves
+      rsum += __shfl_xor(rsum, 32, 64);
+      if (hh == 0) red_row[(i * 2 + wr) * 64 + l_loc] += rsum;
+    }
+
+    // ---- column sums of G over l (lanes and the wc pair) ----
+    {
+      const float cg = half_reduce16(colacc);
+      const int idx = (lane >> 1) & 15;
+      if ((lane & 1) == 0) red_col[wc * 64 + 32 * wr + 8 * (idx >> 2) + 4 * hh + (idx & 3)] = cg;
+    }
+    // ---- dX^T exchange: wave (wr, wc) keeps the p tiles pt % 2 == wc ----
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt)
+      if (pt % 2 != wc) {
+        float* o = xch + ((wr * PT + pt) * 16) * 64 + lane;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[v * 64] = dXT[pt][v];
+      }
+    __syncthreads();
+    floatx16 dXk[PTW];
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      const int pt = 2 * q + wc;
+      zero(dXk[q]);
+      if (pt >= PT) continue;
+      const float* o = xch + ((wr * PT + pt) * 16) * 64 + lane;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dXk[q][v] = dXT[pt][v] + o[v * 64];
+    }
+    if (threadIdx.x < 64) {
+      const int sg = 64 * j + threadIdx.x;
+      if (sg < ci.len) a.colG[((int64_t)c * d.H + h) * Qpad + sg] = red_col[threadIdx.x] + red_col[64 + threadIdx.x];
+    }
+
+    // ---- per-token state terms of column block j (lane = token t_loc) ----
+    const float cs_t = s_cs2[tg];
+    const float dw = cs_last - cs_t;
+    const float ws = t_ok ? exp2_fast(clamp_med3(dw, -SSD_T2, SSD_T2)) : 0.0f;
+    const float pw = fabsf(dw) < SSD_T2 ? 1.0f : 0.0f;
+    const float dts = s_dt[tg];
+    // dX^T += w_s B_s dst^T; E, x.dX, D.dy, dx
+    float esum = 0.0f, xsum = 0.0f, dpart = 0.0f;
+    const bf16* dyc = dYt + j * 64 * PP;
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      const int pt = 2 * q + wc;
+      if (pt >= PT) continue;
+      floatx16 tmp;
+      zero(tmp);
+#pragma unroll
+      for (int kk = 0; kk < NP; kk += 16)
+        mfma(tmp, tld8<NP>(dstT, 32 * pt + l32, kk + 8 * hh), tld8<NP>(Bt, t_loc, kk + 8 * hh));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p0 = 32 * pt + 8 * r + 4 * hh;
+        const bf16x4 xv = tld4<PP>(xj, t_loc, p0);
+        const bf16x4 yv = tld4<PP>(dyc, t_loc, p0);
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * r + e;
+          const float xf = (float)xv[e], yf = (float)yv[e];
+          const float tv = tmp[v] * ws;
+          const float dX = dXk[q][v] + tv;
+          esum += xf * tv;
+          xsum += xf * dX;
+          dpart += xf * yf;
+          o[e] = (bf16)(dts * dX + Dh * yf);
+        }
+        if (t_ok) {
+          bf16* op = a.dx + (int64_t)(ci.row0 + tg) * xrow + (int64_t)h * d.P + p0;
+          if (d.vec_x && p0 + 4 <= d.P) {
+            *reinterpret_cast<bf16x4*>(op) = o;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (p0 + e < d.P) op[e] = o[e];
+          }
+        }
+      }
+    }
+    esum += __shfl_xor(esum, 32, 64);
+    xsum += __shfl_xor(xsum, 32, 64);
+
+    // dB state part: dBs^T[n][s] += w_s dt_s sum_p dst[p][n] x[s][p]
+    // dC Y_off part: dCo^T[n][l] += e^{cs_l} sum_p h_in[p][n] dy[l][p]; dcs_off
+    const float el = t_ok ? exp2_fast(clamp_med3(cs_t, -SSD_T2, SSD_T2)) : 0.0f;
+    const float pl = fabsf(cs_t) < SSD_T2 ? 1.0f : 0.0f;
+    float osum = 0.0f;
+    const bf16* crow = a.Cm + (int64_t)(ci.row0 + (t_ok ? tg : 0)) * brow + (int64_t)g * d.N;
+#pragma unroll
+    for (int ntk = 0; ntk < NTW; ++ntk) {
+      const int nt = 2 * ntk + wc;
+      if (nt >= NT) continue;
+      floatx16 tb, tc;
+      zero(tb);
+      zero(tc);
+#pragma unroll
+      for (int kk = 0; kk < PP; kk += 16) {
+        const bf16x8 xb = tld8<PP>(xj, t_loc, kk + 8 * hh);
+        const bf16x8 yb = tld8<PP>(dyc, t_loc, kk + 8 * hh);
+        mfma(tb, ttr_std<NP>(dstT, kk, 32 * nt), xb);
+        mfma(tc, ttr_std<NP>(hinT, kk, 32 * nt), yb);
+      }
+      const float wsd = ws * dts;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n0 = 32 * nt + 8 * r + 4 * hh;
+        bf16x4 cq;
+        if (t_ok && d.vec_bc && n0 + 4 <= d.N) {
+          cq = *reinterpret_cast<const bf16x4*>(crow + n0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cq[e] = (t_ok && n0 + e < d.N) ? crow[n0 + e] : (bf16)0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * r + e;
+          dBT[ntk][v] = fmaf(tb[v], wsd, dBT[ntk][v]);
+          const float tcv = tc[v] * el;
+          dCoT[ntk][v] += tcv;
+          osum += tcv * (float)cq[e];
+        }
+      }
+    }
+    osum += __shfl_xor(osum, 32, 64);
+    for (int o = 32; o > 0; o >>= 1) dpart += __shfl_xor(dpart, o, 64);
+    if (hh == 0) {
+      red_e[wc * 64 + t_loc] = esum * dts * pw;
+      red_x[wc * 64 + t_loc] = xsum;
+      red_o[wc * 64 + t_loc] = osum * pl;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int tl = threadIdx.x, tgg = 64 * j + tl;
+      if (tgg < ci.len) {
+        const int64_t o = ((int64_t)c * d.H + h) * Qpad + tgg;
+        a.eterm[o] = red_e[tl] + red_e[64 + tl];
+        a.xdx[o] = red_x[tl] + red_x[64 + tl];
+        a.dcs_off[o] = red_o[tl] + red_o[64 + tl];
+      }
+    }
+    for (int e = threadIdx.x; e < nt_i * 64; e += 256) {
+      const int i = j + e / 64, l = e % 64;
+      const int lg = 64 * i + l;
+      if (lg < ci.len)
+        a.rowG[(((int64_t)j * d.max_chunks + c) * d.H + h) * Qpad + lg] =
+            red_row[(i * 2 + 0) * 64 + l] + red_row[(i * 2 + 1) * 64 + l];
+    }
+    __syncthreads();  // red_e / red_o reads done before the dD partials reuse red_o
+    if (lane == 0) red_o[w] = dpart;
+    __syncthreads();
+    if (threadIdx.x == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_o[0] + red_o[1] + red_o[2] + red_o[3];
+  }
+
+  // ---- outputs summed over the slice's heads ----
+  const int64_t sl_off = (int64_t)slc * d.R * brow;
+  float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
+#pragma unroll
+  for (int t = 0; t < kMaxSlots; ++t) {
+    if (t >= nt_i) continue;
+    float* tile = dSbase + (int64_t)((j + t) * nb + j) * 4096;
+    const int l_loc = 32 * wc + l32;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatx4 q;
+      q[0] = dS[t][4 * r + 0];
+      q[1] = dS[t][4 * r + 1];
+      q[2] = dS[t][4 * r + 2];
+      q[3] = dS[t][4 * r + 3];
+      *reinterpret_cast<floatx4*>(tile + l_loc * 64 + 32 * wr + 8 * r + 4 * hh) = q;
+    }
+  }
+  if (t_ok) {
+    float* ob = a.dBs + sl_off + (int64_t)(ci.row0 + tg) * brow + (int64_t)g * d.N;
+    float* oc = a.dCo + sl_off + (int64_t)(ci.row0 + tg) * brow + (int64_t)g * d.N;
+#pragma unroll
+    for (int ntk = 0; ntk < NTW; ++ntk) {
+      const int nt = 2 * ntk + wc;
+      if (nt >= NT) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n0 = 32 * nt + 8 * r + 4 * hh;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n0 + e < d.N) {
+            ob[n0 + e] = dBT[ntk][4 * r + e];
+            oc[n0 + e] = dCoT[ntk][4 * r + e];
+          }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dB and dC of block k of a chunk (one block per (chunk, block, group)):
+//   dC_l = dCo_l + sum_{j <= k} sum_s dS[k,j][l,s] B_s
+//   dB_s = dBs_s + sum_{i >= k} sum_l dS[i,k][l,s] C_l
+// summed over the head slices, computed transposed ([n][token]) on MFMA.
+// ---------------------------------------------------------------------------
+template <int NT>
+__global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* __restrict__ dB,
+                                                bf16* __restrict__ dC) {
+  constexpr int NP = 32 * NT, NTW = (NT + 1) / 2;
+  __shared__ __align__(16) bf16 tBC[64 * NP];
+  __shared__ __align__(16) bf16 tS[64 * 64];
+  const int nb = d.Qpad / 64;
+  const int c = blockIdx.x, kb = blockIdx.y, g = blockIdx.z;
+  const ChunkInfo ci = a.chunks[c];
+  const int nbl = (ci.len + 63) >> 6;
+  if (kb >= nbl) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w & 1, wc = w >> 1;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int64_t brow = (int64_t)d.G * d.N;
+  const int64_t tstride = (int64_t)d.max_chunks * d.G * nb * nb * 4096;  // per slice
+  const float* dSc = a.dS + ((int64_t)c * d.G + g) * (int64_t)(nb * nb) * 4096;
+
+  auto stage_dS = [&](int i, int j) {
+    const float* src = dSc + (int64_t)(i * nb + j) * 4096;
+    for (int id = threadIdx.x; id < 512; id += 256) {  // 8 floats per id
+      const int r = id >> 3, k = (id & 7) * 8;
+      floatx4 s0 = *reinterpret_cast<const floatx4*>(src + r * 64 + k);
+      floatx4 s1 = *reinterpret_cast<const floatx4*>(src + r * 64 + k + 4);
+      for (int sl = 1; sl < a.nslices; ++sl) {
+        const float* p = src + sl * tstride + r * 64 + k;
+        s0 += *reinterpret_cast<const floatx4*>(p);
+        s1 += *reinterpret_cast<const floatx4*>(p + 4);
+      }
+      bf16x8 v;
+      v[0] = (bf16)s0[0]; v[1] = (bf16)s0[1]; v[2] = (bf16)s0[2]; v[3] = (bf16)s0[3];
+      v[4] = (bf16)s1[0]; v[5] = (bf16)s1[1]; v[6] = (bf16)s1[2]; v[7] = (bf16)s1[3];
+      *reinterpret_cast<bf16x8*>(tS + toff<64>(r, k)) = v;
+    }
+  };
+  auto stage_bc = [&](const bf16* src, int blk) {
+    TileStage<64, NP, 256> st;
+    tstage_load(st, src + (int64_t)(ci.row0 + 64 * blk) * brow + (int64_t)g * d.N, brow,
+                min(64, ci.len - 64 * blk), d.N, d.vec_bc);
+    tstage_store(st, tBC);
+  };
+
+  // wave (wr, wc): tokens 32 wr + l32 of block kb, n tiles nt = 2 ntk + wc
+  floatx16 acc[NTW];
+  for (int pass = 0; pass < 2; ++pass) {
+    // pass 0: dC (tiles (kb, j), j <= kb, with B_j); pass 1: dB (tiles (i, kb), i >= kb, with C_i)
+#pragma unroll
+    for (int q = 0; q < NTW; ++q) zero(acc[q]);
+    const int lo = pass == 0 ? 0 : kb, hi = pass == 0 ? kb : nbl - 1;
+    for (int m = lo; m <= hi; ++m) {
+      __syncthreads();
+      if (pass == 0) {
+        stage_dS(kb, m);
+        stage_bc(a.Bm, m);
+      } else {
+        stage_dS(m, kb);
+        stage_bc(a.Cm, m);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < NTW; ++q) {
+        const int nt = 2 * q + wc;
+        if (nt >= NT) continue;
+#pragma unroll
+        for (int kk = 0; kk < 64; kk += 16) {
+          const bf16x8 av = ttr_std<NP>(tBC, kk, 32 * nt);
+          // pass 0: B[k = s][j = l] = dS[l][s] (row l, natural); pass 1: B[k = l][j = s] (transposed)
+          const bf16x8 bv = pass == 0 ? tld8<64>(tS, 32 * wr + l32, kk + 8 * hh) : ttr_std<64>(tS, kk, 32 * wr);
+          mfma(acc[q], av, bv);
+        }
+      }
+    }
+    const int tok = 64 * kb + 32 * wr + l32;
+    if (tok < ci.len) {
+      const float* extra = pass == 0 ? a.dCo : a.dBs;
+      bf16* out = pass == 0 ? dC : dB;
+      const int64_t row = (int64_t)(ci.row0 + tok) * brow + (int64_t)g * d.N;
+#pragma unroll
+      for (int q = 0; q < NTW; ++q) {
+        const int nt = 2 * q + wc;
+        if (nt >= NT) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n0 = 32 * nt + 8 * r + 4 * hh;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n0 + e >= d.N) continue;
+            float v = acc[q][4 * r + e];
+            for (int sl = 0; sl < a.nslices; ++sl) v += extra[(int64_t)sl * d.R * brow + row + n0 + e];
+            out[row + n0 + e] = (bf16)v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+bool bwd_main_supported(int dtype, const SsdDims& d) {
+  return dtype == 1 && d.Ppad <= 64 && d.Qpad <= 256 && d.Npad <= 128;
+}
+
+size_t lds_bwd_main(const SsdDims& d) {
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return BwdMainLds<1, 1>::bytes(d.Qpad);
+    case 12: return BwdMainLds<1, 2>::bytes(d.Qpad);
+    case 14: return BwdMainLds<1, 4>::bytes(d.Qpad);
+    case 21: return BwdMainLds<2, 1>::bytes(d.Qpad);
+    case 22: return BwdMainLds<2, 2>::bytes(d.Qpad);
+    default: return BwdMainLds<2, 4>::bytes(d.Qpad);
+  }
+}
+
+template <int PT, int NT>
+static hipError_t bwd_main_t(const SsdDims& d, const BwdMainArgs& a, hipStream_t s) {
+  const int U = d.max_chunks * d.G * a.nslices;
+  const int blocks = (U + 7) / 8 * 8 * (d.Qpad / 64);
+  const size_t lds = BwdMainLds<PT, NT>::bytes(d.Qpad);
+  ensure_lds(k_bwd_main<PT, NT>, lds);
+  hipLaunchKernelGGL((k_bwd_main<PT, NT>), dim3(blocks), dim3(256), lds, s, d, a);
+  return hipGetLastError();
+}
+
+template <int NT>
+static hipError_t bwd_bc_t(const SsdDims& d, const BwdMainArgs& a, void* dB, void* dC, hipStream_t s) {
+  dim3 grid(d.max_chunks, d.Qpad / 64, d.G);
+  hipLaunchKernelGGL((k_bwd_bc<NT>), grid, dim3(256), 0, s, d, a, reinterpret_cast<bf16*>(dB),
+                     reinterpret_cast<bf16*>(dC));
+  return hipGetLastError();
+}
+
+static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx) {
+  BwdMainArgs a;
+  a.chunks = b.chunks;
+  a.cs = b.cs;
+  a.hin = reinterpret_cast<const bf16*>(b.hin);
+  a.dst = b.dst;
+  a.x = reinterpret_cast<const bf16*>(in.x);
+  a.dt = in.dt;
+  a.Bm = reinterpret_cast<const bf16*>(in.B);
+  a.Cm = reinterpret_cast<const bf16*>(in.C);
+  a.Dv = in.D;
+  a.dy = reinterpret_cast<const bf16*>(dy);
+  a.dx = reinterpret_cast<bf16*>(dx);
+  a.rowG = b.rowG;
+  a.colG = b.colG;
+  a.eterm = b.eterm;
+  a.xdx = b.xdx;
+  a.dcs_off = b.dcs_off;
+  a.dD_part = b.dD_part;
+  a.dS = b.dS_tiles;
+  a.dBs = b.dB_part;
+  a.dCo = b.dC_part;
+  a.nslices = b.nslices;
+  a.hslice = b.hslice;
+  return a;
+}
+
+hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+                           hipStream_t s) {
+  const BwdMainArgs a = make_main_args(d, b, in, dy, dx);
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return bwd_main_t<1, 1>(d, a, s);
+    case 12: return bwd_main_t<1, 2>(d, a, s);
+    case 14: return bwd_main_t<1, 4>(d, a, s);
+    case 21: return bwd_main_t<2, 1>(d, a, s);
+    case 22: return bwd_main_t<2, 2>(d, a, s);
+    default: return bwd_main_t<2, 4>(d, a, s);
+  }
+}
+
+hipError_t launch_bwd_bc(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* dB, void* dC, hipStream_t s) {
+  const BwdMainArgs a = make_main_args(d, b, in, nullptr, nullptr);
+  switch (d.Npad / 32) {
+    case 1: return bwd_bc_t<1>(d, a, dB, dC, s);
+    case 2: return bwd_bc_t<2>(d, a, dB, dC, s);
+    default: return bwd_bc_t<4>(d, a, dB, dC, s);
+  }
+}
+
+int bwd_main_num_sets(const SsdDims& d) { return d.Qpad / 64; }

@@ -23,7 +23,8 @@ struct Plan {
   // byte offsets inside each workspace
   size_t o_chunks, o_seq0, o_cs, o_hin, o_ypre, o_rstd, saved_bytes;
   size_t o_st, fwd_bytes;
-  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, bwd_bytes;
+  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, bwd_bytes;
+  int fused_bwd, nrowg;
 };
 
 int plan(const ssd_desc_t* s, Plan* p) {
@@ -66,13 +67,24 @@ int plan(const ssd_desc_t* s, Plan* p) {
   d.eps = s->norm_eps;
   p->dtype = s->dtype;
   p->state_dtype = s->state_dtype;
-  if (lds_chunk_scan_fwd(p->dtype, d) > kMaxLds || lds_bwd_col(p->dtype, d) > kMaxLds ||
-      lds_bwd_row(p->dtype, d) > kMaxLds)
+  p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
+  if (lds_chunk_scan_fwd(p->dtype, d) > kMaxLds ||
+      (p->fused_bwd ? lds_bwd_main(d) > kMaxLds
+                    : (lds_bwd_col(p->dtype, d) > kMaxLds || lds_bwd_row(p->dtype, d) > kMaxLds)))
     return SSD_ERR_UNSUPPORTED;
 
   // head slices of the backward: enough blocks to fill the chip, fewest partials
-  const int64_t per_slice = max_chunks * d.G * (d.Qpad / SSD_BLK);
-  int64_t ns = (2048 + per_slice - 1) / per_slice;
+  int64_t ns;
+  if (p->fused_bwd) {
+    // one block per (chunk, group, slice, column set); about one block per CU
+    p->nrowg = bwd_main_num_sets(d);
+    const int64_t per_slice = max_chunks * d.G * p->nrowg;
+    ns = (256 + per_slice - 1) / per_slice;
+  } else {
+    p->nrowg = 1;
+    const int64_t per_slice = max_chunks * d.G * (d.Qpad / SSD_BLK);
+    ns = (2048 + per_slice - 1) / per_slice;
+  }
   if (ns < 1) ns = 1;
   if (ns > d.hpg) ns = d.hpg;
   p->hslice = (d.hpg + ns - 1) / ns;
@@ -98,7 +110,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_dyp = d.has_z ? take((size_t)R * H * d.P * es) : 0;
   p->o_dst = take(MC * H * PN * sizeof(float));
   p->o_dtot = take(MC * H * p->npass_blk * sizeof(float));
-  p->o_rowG = take(MC * H * d.Qpad * sizeof(float));
+  p->o_rowG = take((size_t)p->nrowg * MC * H * d.Qpad * sizeof(float));
   p->o_colG = take(MC * H * d.Qpad * sizeof(float));
   p->o_eterm = take(MC * H * d.Qpad * sizeof(float));
   p->o_dcs = take(MC * H * d.Qpad * sizeof(float));
@@ -106,8 +118,11 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_dD = take(MC * H * (d.Qpad / SSD_BLK) * sizeof(float));
   p->o_dA = take(MC * H * sizeof(float));
   const size_t bcn = (size_t)R * d.G * d.N * sizeof(float);
-  p->o_dBp = p->nslices > 1 ? take(p->nslices * bcn) : 0;
-  p->o_dCp = p->nslices > 1 ? take(p->nslices * bcn) : 0;
+  const bool parts = p->fused_bwd || p->nslices > 1;
+  p->o_dBp = parts ? take(p->nslices * bcn) : 0;
+  p->o_dCp = parts ? take(p->nslices * bcn) : 0;
+  const size_t nbq = (size_t)(d.Qpad / SSD_BLK);
+  p->o_dS = p->fused_bwd ? take((size_t)p->nslices * MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
   p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
   p->bwd_bytes = off;
   return SSD_OK;
@@ -125,6 +140,8 @@ void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
   b->nslices = (int)p.nslices;
   b->hslice = (int)p.hslice;
   b->norm_blocks = (int)p.norm_blocks;
+  b->fused_bwd = p.fused_bwd;
+  b->nrowg = p.nrowg;
 }
 
 void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
@@ -139,8 +156,10 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->xdx = reinterpret_cast<float*>(s + p.o_xdx);
   b->dD_part = reinterpret_cast<float*>(s + p.o_dD);
   b->dA_part = reinterpret_cast<float*>(s + p.o_dA);
-  b->dB_part = p.nslices > 1 ? reinterpret_cast<float*>(s + p.o_dBp) : nullptr;
-  b->dC_part = p.nslices > 1 ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
+  const bool parts = p.fused_bwd || p.nslices > 1;
+  b->dB_part = parts ? reinterpret_cast<float*>(s + p.o_dBp) : nullptr;
+  b->dC_part = parts ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
+  b->dS_tiles = p.fused_bwd ? reinterpret_cast<float*>(s + p.o_dS) : nullptr;
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
 }
 
@@ -264,12 +283,18 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   SSD_PHASE(tm, SSD_PH_BWD_PASS,
             launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
                                   d.has_init ? a->dinit : nullptr, s));
-  SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));
-  SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, d, b, in, dY, a->dC, s));
+  if (p.fused_bwd) {
+    // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
+    SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_main(d, b, in, dY, a->dx, s));
+    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_bc(d, b, in, a->dB, a->dC, s));
+  } else {
+    SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));
+    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, d, b, in, dY, a->dC, s));
+  }
   SSD_PHASE(tm, SSD_PH_BWD_FINISH,
             launch_bwd_finish(p.dtype, d, b, in, d.has_dt ? a->ddt : nullptr,
                               d.a_mode == SSD_A_PER_TOKEN ? a->dA : nullptr, s));
-  if (p.nslices > 1) {
+  if (p.nslices > 1 && !p.fused_bwd) {
     const int64_t nelem = d.R * d.G * d.N;
     SSD_TRY(tm.begin(SSD_PH_BWD_REDUCE_BC));
     SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dB_part, a->dB, s));

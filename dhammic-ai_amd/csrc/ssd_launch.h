@@ -55,6 +55,14 @@ hipError_t launch_bwd_finish(int dtype, const SsdDims& d, const SsdBufs& b, cons
 size_t lds_bwd_col(int dtype, const SsdDims& d);
 size_t lds_bwd_row(int dtype, const SsdDims& d);
 
+// ssd_bwd_main.hip (fused backward, bf16, Ppad <= 64, Qpad <= 256)
+bool bwd_main_supported(int dtype, const SsdDims& d);
+size_t lds_bwd_main(const SsdDims& d);
+int bwd_main_num_sets(const SsdDims& d);
+hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+                           hipStream_t s);
+hipError_t launch_bwd_bc(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* dB, void* dC, hipStream_t s);
+
 // ssd_norm.hip
 hipError_t launch_gated_norm_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
                                  void* y, hipStream_t s);

@@ -1,0 +1,225 @@
+// bf16 LDS tiles and MFMA operand access for gfx950 (wave64).
+//
+// A tile is ROWS x W bf16 (W = 32, 64 or 128 elements per row), stored row
+// after row with no padding; inside a row the 16-byte chunks are permuted by
+// an XOR with a per-row value, so that
+//   * eight consecutive rows read at the same column chunk (the k-contiguous
+//     operand read of v_mfma_f32_32x32x16_bf16) hit eight different bank
+//     groups, and
+//   * four consecutive rows read as 32 contiguous bytes each (one 16-lane
+//     group of ds_read_b64_tr_b16) hit four different bank-group pairs.
+//
+// Operand conventions of v_mfma_f32_32x32x16_bf16 (used throughout):
+//   A[i][k]: lane L supplies i = L % 32, k = 8 * (L / 32) + t, t = 0..7
+//   B[k][j]: lane L supplies j = L % 32, k = 8 * (L / 32) + t
+//   D[i][j]: lane L, register v holds i = 8 * (v / 4) + 4 * (L / 32) + v % 4, j = L % 32
+//
+// ds_read_b64_tr_b16 (measured lane layout): inside each 16-lane group, lane q
+// receives element q % 4 of the 8-byte loads of lanes 4e + q / 4, e = 0..3.
+// So if lane q of a group loads row kb + q / 4, columns m0 + 4 * (q % 4) .. +3,
+// lane q ends up holding column m0 + q of rows kb .. kb + 3: a k-contiguous
+// operand read from a tile whose rows are the contraction index.
+#pragma once
+
+#include "ssd_common.h"
+
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int W>
+__device__ __forceinline__ int tswz(int r) {
+  static_assert(W == 32 || W == 64 || W == 128, "tile width");
+  if constexpr (W == 32) return (((r >> 1) & 1) << 1) | ((r >> 2) & 1);
+  else return ((r & 3) << 1) | ((r >> 2) & 1);
+}
+
+// Element offset of (row r, column k) in a W-wide tile.
+template <int W>
+__device__ __forceinline__ int toff(int r, int k) {
+  return r * W + ((((k >> 3) ^ tswz<W>(r))) << 3) + (k & 7);
+}
+
+// Eight consecutive columns k .. k+7 (k % 8 == 0) of row r.
+template <int W>
+__device__ __forceinline__ bf16x8 tld8(const bf16* t, int r, int k) {
+  return *reinterpret_cast<const bf16x8*>(t + toff<W>(r, k));
+}
+
+// Four consecutive columns k .. k+3 (k % 4 == 0) of row r.
+template <int W>
+__device__ __forceinline__ bf16x4 tld4(const bf16* t, int r, int k) {
+  return *reinterpret_cast<const bf16x4*>(t + toff<W>(r, k));
+}
+
+// Rows kb .. kb+3 of column m0 + (lane % 16) (m0 % 16 == 0, kb % 4 == 0).
+template <int W>
+__device__ __forceinline__ bf16x4 ttr4(const bf16* t, int kb, int m0) {
+  const int q = threadIdx.x & 15;
+  const bf16* p = t + toff<W>(kb + (q >> 2), m0 + ((q & 3) << 2));
+  const shortx4 v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// k-contiguous operand (A[i][k] with i = mbase + lane % 32, or B[k][j] with
+// j = mbase + lane % 32), k = k0 + 8 * (lane / 32) + t, read from a tile whose
+// row index is k and column index is i (or j).
+template <int W>
+__device__ __forceinline__ bf16x8 ttr_std(const bf16* t, int k0, int mbase) {
+  const int L = threadIdx.x & 63, h = L >> 5;
+  const int m0 = mbase + (((L >> 4) & 1) << 4);
+  return cat8(ttr4<W>(t, k0 + 8 * h, m0), ttr4<W>(t, k0 + 8 * h + 4, m0));
+}
+
+// Operand partner of an accumulator tile reused in place (see acc_frag): for
+// MFMA step kk over the 32 rows k0 .. k0+31, lane L supplies the rows
+// k0 + 16 kk + 8 (t / 4) + 4 (L / 32) + t % 4, the order in which the
+// accumulator registers 8 kk .. 8 kk + 7 hold them.
+template <int W>
+__device__ __forceinline__ bf16x8 ttr_perm(const bf16* t, int k0, int kk, int mbase) {
+  const int L = threadIdx.x & 63, h = L >> 5;
+  const int m0 = mbase + (((L >> 4) & 1) << 4);
+  return cat8(ttr4<W>(t, k0 + 16 * kk + 4 * h, m0), ttr4<W>(t, k0 + 16 * kk + 8 + 4 * h, m0));
+}
+
+// Registers 8 kk .. 8 kk + 7 of an accumulator tile X, as bf16: used as the B
+// operand this is B[k][j] = X[row(8 kk + t)][j]; used as the A operand it is
+// A[i][k] = X[row(8 kk + t)][i] (X transposed). The partner operand must list
+// its k in the same row order (ttr_perm).
+__device__ __forceinline__ bf16x8 acc_frag(const floatx16& x, int kk) {
+  bf16x8 f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) f[t] = (bf16)x[8 * kk + t];
+  return f;
+}
+
+__device__ __forceinline__ void mfma(floatx16& acc, const bf16x8& a, const bf16x8& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Global -> LDS staging of a ROWS x W bf16 tile from a row-major tensor, with
+// rows >= nrows and columns >= width zero-filled. Thread t handles 16-byte
+// vectors t, t + NTHR, ... (row-major order, so a wave reads whole rows).
+// `vec` (uniform): 16-byte global loads are aligned (width, row stride and
+// column offset multiples of 8 elements, 16-byte aligned base).
+// ---------------------------------------------------------------------------
+template <int ROWS, int W, int NTHR>
+struct TileStage {
+  static constexpr int NVEC = ROWS * W / 8;
+  static constexpr int PER = (NVEC + NTHR - 1) / NTHR;
+  bf16x8 v[PER];
+};
+
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_load(TileStage<ROWS, W, NTHR>& s, const bf16* __restrict__ g, int64_t ld,
+                                            int nrows, int width, bool vec) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      const bf16* p = g + (int64_t)r * ld + k;
+      bf16x8 v;
+      if (r < nrows && vec && k < width) {
+        v = *reinterpret_cast<const bf16x8*>(p);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (r < nrows && k + e < width) ? p[e] : (bf16)0.0f;
+      }
+      s.v[q] = v;
+    }
+  }
+}
+
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, bf16* t) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = s.v[q];
+    }
+  }
+}
+
+// Same, from an fp32 row-major source (converted to bf16); rows of `ld` floats,
+// 16-byte aligned rows (ld % 4 == 0, W <= ld).
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_load_f32(TileStage<ROWS, W, NTHR>& s, const float* __restrict__ g,
+                                                int64_t ld) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      const float* p = g + (int64_t)r * ld + k;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(p);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(p + 4);
+      bf16x8 v;
+      v[0] = (bf16)a[0]; v[1] = (bf16)a[1]; v[2] = (bf16)a[2]; v[3] = (bf16)a[3];
+      v[4] = (bf16)b[0]; v[5] = (bf16)b[1]; v[6] = (bf16)b[2]; v[7] = (bf16)b[3];
+      s.v[q] = v;
+    }
+  }
+}
+
+// exp2 of a value already clamped; the decays below are all exp(clamp(d, -20, 20))
+// evaluated as exp2(clamp(d * log2 e, +-20 log2 e)).
+__device__ __forceinline__ float exp2_fast(float v) { return __builtin_amdgcn_exp2f(v); }
+__device__ __forceinline__ float clamp_med3(float v, float lo, float hi) { return __builtin_amdgcn_fmed3f(v, lo, hi); }
+
+#define SSD_LOG2E 1.4426950408889634f
+#define SSD_T2 (20.0f * SSD_LOG2E)
+
+// Sum of v over the 32 lanes of each half-wave, for 16 values at once.
+// Afterwards lane L holds, in out, the sum of v[(L >> 1) & 15] over its half.
+__device__ __forceinline__ float half_reduce16(float (&v)[16]) {
+  const int L = threadIdx.x & 63;
+  float a[8];
+  {
+    const bool b = (L >> 4) & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float send = b ? v[k] : v[k + 8];
+      const float keep = b ? v[k + 8] : v[k];
+      a[k] = keep + __shfl_xor(send, 16, 64);
+    }
+  }
+  float c[4];
+  {
+    const bool b = (L >> 3) & 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float send = b ? a[k] : a[k + 4];
+      const float keep = b ? a[k + 4] : a[k];
+      c[k] = keep + __shfl_xor(send, 8, 64);
+    }
+  }
+  float e[2];
+  {
+    const bool b = (L >> 2) & 1;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float send = b ? c[k] : c[k + 2];
+      const float keep = b ? c[k + 2] : c[k];
+      e[k] = keep + __shfl_xor(send, 4, 64);
+    }
+  }
+  float f;
+  {
+    const bool b = (L >> 1) & 1;
+    const float send = b ? e[0] : e[1];
+    const float keep = b ? e[1] : e[0];
+    f = keep + __shfl_xor(send, 2, 64);
+  }
+  return f + __shfl_xor(f, 1, 64);
+}
