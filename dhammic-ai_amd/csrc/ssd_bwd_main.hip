@@ -33,7 +33,7 @@ struct BwdMainArgs {
   const ChunkInfo* chunks;
   const float* cs;    // [MC][H][Qpad]
   const bf16* hin;    // [MC][H][Ppad][Npad]
-  const float* dst;   // [MC][H][Ppad][Npad]
+  const bf16* dst;    // [MC][H][Ppad][Npad], gradient leaving each chunk (bf16)
   const bf16* x;
   const float* dt;
   const bf16* Bm;
@@ -61,8 +61,8 @@ struct BwdMainLds {
   static constexpr int RED = 1024;  // floats of reduction scratch
   static size_t bytes(int Qpad) {
     const size_t xch = 2 * PT * 4096;
-    return sizeof(float) * (2 * Qpad + RED) + 2 * (size_t)(64 * PP + 4 * 64 * PP + 2 * PP * NP + 64 * NP + 4 * 1024) +
-           xch;
+    return sizeof(float) * (2 * Qpad + RED) +
+           2 * (size_t)(5 * tsize<64, PP>() + 2 * tsize<PP, NP>() + tsize<64, NP>() + 4 * tsize<32, 32>()) + xch;
   }
 };
 
@@ -94,8 +94,8 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
   if (h_lo >= h_hi) return;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w & 1, wc = w >> 1;
-  const int hh = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wr = w & 1, wc = w >> 1;
+  int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
   const int Qpad = d.Qpad;
   const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
 
@@ -107,19 +107,20 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   float* red_e = red + 640;                        // [2 wc][64]
   float* red_x = red + 768;                        // [2 wc][64]
   float* red_o = red + 896;                        // [2 wc][64] (the first 4 also hold the dD partials)
+  constexpr int XT = tsize<64, PP>(), ST = tsize<PP, NP>(), BTS = tsize<64, NP>(), MT = tsize<32, 32>();
   bf16* xj = reinterpret_cast<bf16*>(red + BwdMainLds<PT, NT>::RED);  // [64][PP]
-  bf16* dYt = xj + 64 * PP;                        // [4][64][PP] (blocks j .. nbl-1 used)
-  bf16* dstT = dYt + 4 * 64 * PP;                  // [PP][NP]
-  bf16* hinT = dstT + PP * NP;                     // [PP][NP]
-  bf16* Bt = hinT + PP * NP;                       // [64][NP]
-  bf16* Mb = Bt + 64 * NP + w * 1024;              // this wave's [32][32]
-  float* xch = reinterpret_cast<float*>(Bt + 64 * NP + 4 * 1024);
+  bf16* dYt = xj + XT;                             // [4][64][PP] (blocks j .. nbl-1 used)
+  bf16* dstT = dYt + 4 * XT;                       // [PP][NP]
+  bf16* hinT = dstT + ST;                          // [PP][NP]
+  bf16* Bt = hinT + ST;                            // [64][NP]
+  bf16* Mb = Bt + BTS + w * MT;                    // this wave's [32][32]
+  float* xch = reinterpret_cast<float*>(Bt + BTS + 4 * MT);
 
   // ---- B tile of column block j ----
   {
     TileStage<64, NP, 256> st;
-    tstage_load(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
-                min(64, ci.len - 64 * j), d.N, d.vec_bc);
+    tstage_load_v(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
+                min(64, ci.len - 64 * j), d.N);
     tstage_store(st, Bt);
   }
   __syncthreads();
@@ -144,12 +145,9 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     for (int kk = 0; kk < NP; kk += 16) {
       const int n0 = kk + 8 * hh;
       bf16x8 cb;
-      if (lok && d.vec_bc && n0 < d.N) {
-        cb = *reinterpret_cast<const bf16x8*>(crow + n0);
-      } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) cb[e] = (lok && n0 + e < d.N) ? crow[n0 + e] : (bf16)0.0f;
-      }
+      for (int e = 0; e < 8; ++e) cb[e] = (bf16)0.0f;
+      if (lok && n0 < d.N) cb = *reinterpret_cast<const bf16x8*>(crow + n0);
       mfma(sacc, tld8<NP>(Bt, 32 * wr + l32, n0), cb);
     }
     S[t][0] = acc_frag(sacc, 0);
@@ -168,27 +166,40 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   }
 
   for (int h = h_lo; h < h_hi; ++h) {
-    __syncthreads();  // the previous head's LDS reads are done
+    lane = opaque_lane();
+    hh = lane >> 5;
+    l32 = lane & 31;
     {
+      // every global load of the head is issued before the first LDS store
       const float* csc = a.cs + ((int64_t)c * d.H + h) * Qpad;
-      for (int l = threadIdx.x; l < Qpad; l += 256) {
-        s_cs2[l] = csc[l] * SSD_LOG2E;
-        s_dt[l] = (d.has_dt && l < ci.len) ? a.dt[(int64_t)(ci.row0 + l) * d.H + h] : 1.0f;
+      const int l0 = threadIdx.x;
+      float csv = 0.0f, dtv = 1.0f;
+      if (l0 < Qpad) {
+        csv = csc[l0];
+        if (d.has_dt && l0 < ci.len) dtv = a.dt[(int64_t)(ci.row0 + l0) * d.H + h];
+      }
+      TileStage<64, PP, 256> sx;
+      tstage_load_v(sx, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + (int64_t)h * d.P, xrow,
+                    min(64, ci.len - 64 * j), d.P);
+      TileStage<64, PP, 256> sy[kMaxSlots];
+#pragma unroll
+      for (int t = 0; t < kMaxSlots; ++t)
+        if (t < nt_i)
+          tstage_load_v(sy[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + (int64_t)h * d.P, xrow,
+                        min(64, ci.len - 64 * (j + t)), d.P);
+      TileStage<PP, NP, 256> sd, sh;
+      tstage_load_v(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+      tstage_load_v(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+      __syncthreads();  // the previous head's LDS reads are done
+      if (l0 < Qpad) {
+        s_cs2[l0] = csv * SSD_LOG2E;
+        s_dt[l0] = dtv;
       }
       for (int e = threadIdx.x; e < 4 * 2 * 64; e += 256) red_row[e] = 0.0f;
-      TileStage<64, PP, 256> sx;
-      tstage_load(sx, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + (int64_t)h * d.P, xrow,
-                  min(64, ci.len - 64 * j), d.P, d.vec_x);
-      TileStage<PP, NP, 256> sd, sh;
-      tstage_load_f32(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP);
-      tstage_load(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP, true);
-      for (int i = j; i < nbl; ++i) {
-        TileStage<64, PP, 256> st;
-        tstage_load(st, a.dy + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
-                    min(64, ci.len - 64 * i), d.P, d.vec_x);
-        tstage_store(st, dYt + i * 64 * PP);
-      }
       tstage_store(sx, xj);
+#pragma unroll
+      for (int t = 0; t < kMaxSlots; ++t)
+        if (t < nt_i) tstage_store(sy[t], dYt + (j + t) * XT);
       tstage_store(sd, dstT);
       tstage_store(sh, hinT);
     }
@@ -210,7 +221,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       const int i = j + t;
       const bool diag = t == 0;
       if (diag && wr == 1 && wc == 0) continue;
-      const bf16* dyi = dYt + i * 64 * PP;
+      const bf16* dyi = dYt + i * XT;
       floatx16 dm;
       zero(dm);
 #pragma unroll
@@ -251,9 +262,9 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       // dX^T[p][s] += sum_l dy_i[l][p] M[l][s]  (l over this wave's 32-row window)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 mb = ttr_std<32>(Mb, 16 * kk, 0);
+        const bf16x8 mb = ttr_std<32>(Mb, 16 * kk, 0, lane);
 #pragma unroll
-        for (int pt = 0; pt < PT; ++pt) mfma(dXT[pt], ttr_std<PP>(dyi, 32 * wc + 16 * kk, 32 * pt), mb);
+        for (int pt = 0; pt < PT; ++pt) mfma(dXT[pt], ttr_std<PP>(dyi, 32 * wc + 16 * kk, 32 * pt, lane), mb);
       }
       // row sums of G: per lane over its 16 s rows, then the two half-waves
       rsum += __shfl_xor(rsum, 32, 64);
@@ -262,7 +273,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
 
     // ---- column sums of G over l (lanes and the wc pair) ----
     {
-      const float cg = half_reduce16(colacc);
+      const float cg = half_reduce16(colacc, lane);
       const int idx = (lane >> 1) & 15;
       if ((lane & 1) == 0) red_col[wc * 64 + 32 * wr + 8 * (idx >> 2) + 4 * hh + (idx & 3)] = cg;
     }
@@ -298,7 +309,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     const float dts = s_dt[tg];
     // dX^T += w_s B_s dst^T; E, x.dX, D.dy, dx
     float esum = 0.0f, xsum = 0.0f, dpart = 0.0f;
-    const bf16* dyc = dYt + j * 64 * PP;
+    const bf16* dyc = dYt + j * XT;
 #pragma unroll
     for (int q = 0; q < PTW; ++q) {
       const int pt = 2 * q + wc;
@@ -325,16 +336,8 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
           dpart += xf * yf;
           o[e] = (bf16)(dts * dX + Dh * yf);
         }
-        if (t_ok) {
-          bf16* op = a.dx + (int64_t)(ci.row0 + tg) * xrow + (int64_t)h * d.P + p0;
-          if (d.vec_x && p0 + 4 <= d.P) {
-            *reinterpret_cast<bf16x4*>(op) = o;
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (p0 + e < d.P) op[e] = o[e];
-          }
-        }
+        if (t_ok && p0 < d.P)
+          *reinterpret_cast<bf16x4*>(a.dx + (int64_t)(ci.row0 + tg) * xrow + (int64_t)h * d.P + p0) = o;
       }
     }
     esum += __shfl_xor(esum, 32, 64);
@@ -357,20 +360,17 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       for (int kk = 0; kk < PP; kk += 16) {
         const bf16x8 xb = tld8<PP>(xj, t_loc, kk + 8 * hh);
         const bf16x8 yb = tld8<PP>(dyc, t_loc, kk + 8 * hh);
-        mfma(tb, ttr_std<NP>(dstT, kk, 32 * nt), xb);
-        mfma(tc, ttr_std<NP>(hinT, kk, 32 * nt), yb);
+        mfma(tb, ttr_std<NP>(dstT, kk, 32 * nt, lane), xb);
+        mfma(tc, ttr_std<NP>(hinT, kk, 32 * nt, lane), yb);
       }
       const float wsd = ws * dts;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n0 = 32 * nt + 8 * r + 4 * hh;
         bf16x4 cq;
-        if (t_ok && d.vec_bc && n0 + 4 <= d.N) {
-          cq = *reinterpret_cast<const bf16x4*>(crow + n0);
-        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) cq[e] = (t_ok && n0 + e < d.N) ? crow[n0 + e] : (bf16)0.0f;
-        }
+        for (int e = 0; e < 4; ++e) cq[e] = (bf16)0.0f;
+        if (t_ok && n0 < d.N) cq = *reinterpret_cast<const bf16x4*>(crow + n0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int v = 4 * r + e;
@@ -460,8 +460,8 @@ template <int NT>
 __global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* __restrict__ dB,
                                                 bf16* __restrict__ dC) {
   constexpr int NP = 32 * NT, NTW = (NT + 1) / 2;
-  __shared__ __align__(16) bf16 tBC[64 * NP];
-  __shared__ __align__(16) bf16 tS[64 * 64];
+  __shared__ __align__(16) bf16 tBC[tsize<64, NP>()];
+  __shared__ __align__(16) bf16 tS[tsize<64, 64>()];
   const int nb = d.Qpad / 64;
   const int c = blockIdx.x, kb = blockIdx.y, g = blockIdx.z;
   const ChunkInfo ci = a.chunks[c];
@@ -492,8 +492,8 @@ __global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* 
   };
   auto stage_bc = [&](const bf16* src, int blk) {
     TileStage<64, NP, 256> st;
-    tstage_load(st, src + (int64_t)(ci.row0 + 64 * blk) * brow + (int64_t)g * d.N, brow,
-                min(64, ci.len - 64 * blk), d.N, d.vec_bc);
+    tstage_load_v(st, src + (int64_t)(ci.row0 + 64 * blk) * brow + (int64_t)g * d.N, brow,
+                min(64, ci.len - 64 * blk), d.N);
     tstage_store(st, tBC);
   };
 
@@ -520,9 +520,9 @@ __global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* 
         if (nt >= NT) continue;
 #pragma unroll
         for (int kk = 0; kk < 64; kk += 16) {
-          const bf16x8 av = ttr_std<NP>(tBC, kk, 32 * nt);
+          const bf16x8 av = ttr_std<NP>(tBC, kk, 32 * nt, lane);
           // pass 0: B[k = s][j = l] = dS[l][s] (row l, natural); pass 1: B[k = l][j = s] (transposed)
-          const bf16x8 bv = pass == 0 ? tld8<64>(tS, 32 * wr + l32, kk + 8 * hh) : ttr_std<64>(tS, kk, 32 * wr);
+          const bf16x8 bv = pass == 0 ? tld8<64>(tS, 32 * wr + l32, kk + 8 * hh) : ttr_std<64>(tS, kk, 32 * wr, lane);
           mfma(acc[q], av, bv);
         }
       }
@@ -555,8 +555,10 @@ __global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Shapes of the fused path; at launch it also needs 16-byte vector access
+// (d.vec_x, d.vec_bc), otherwise ssd_bwd runs the column / row kernels.
 bool bwd_main_supported(int dtype, const SsdDims& d) {
-  return dtype == 1 && d.Ppad <= 64 && d.Qpad <= 256 && d.Npad <= 128;
+  return dtype == 1 && d.Ppad <= 64 && d.Qpad <= 256 && d.Npad <= 128 && d.P % 8 == 0 && d.N % 8 == 0;
 }
 
 size_t lds_bwd_main(const SsdDims& d) {
@@ -593,7 +595,7 @@ static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdI
   a.chunks = b.chunks;
   a.cs = b.cs;
   a.hin = reinterpret_cast<const bf16*>(b.hin);
-  a.dst = b.dst;
+  a.dst = b.dst16;
   a.x = reinterpret_cast<const bf16*>(in.x);
   a.dt = in.dt;
   a.Bm = reinterpret_cast<const bf16*>(in.B);

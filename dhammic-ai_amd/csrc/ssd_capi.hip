@@ -23,7 +23,7 @@ struct Plan {
   // byte offsets inside each workspace
   size_t o_chunks, o_seq0, o_cs, o_hin, o_ypre, o_rstd, saved_bytes;
   size_t o_st, fwd_bytes;
-  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, bwd_bytes;
+  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dst16, bwd_bytes;
   int fused_bwd, nrowg;
 };
 
@@ -123,6 +123,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_dCp = parts ? take(p->nslices * bcn) : 0;
   const size_t nbq = (size_t)(d.Qpad / SSD_BLK);
   p->o_dS = p->fused_bwd ? take((size_t)p->nslices * MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
+  p->o_dst16 = p->fused_bwd ? take(MC * H * PN * 2) : 0;
   p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
   p->bwd_bytes = off;
   return SSD_OK;
@@ -160,6 +161,7 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->dB_part = parts ? reinterpret_cast<float*>(s + p.o_dBp) : nullptr;
   b->dC_part = parts ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
   b->dS_tiles = p.fused_bwd ? reinterpret_cast<float*>(s + p.o_dS) : nullptr;
+  b->dst16 = p.fused_bwd ? reinterpret_cast<bf16*>(s + p.o_dst16) : nullptr;
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
 }
 
@@ -272,6 +274,12 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   bind_bwd(p, scratch, &b);
   SsdIn in = {a->x, a->dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
   const PhaseTimer tm{a->events, s};
+  // the fused backward needs 16-byte vector access; otherwise the column / row kernels run
+  const bool fused = p.fused_bwd && d.vec_x && d.vec_bc;
+  if (!fused) {
+    b.nrowg = 1;           // column / row kernels write one rowG partial
+    b.dst16 = nullptr;     // and read dst in fp32
+  }
   const void* dY = a->dy;
   if (d.has_z) {
     SSD_PHASE(tm, SSD_PH_NORM_BWD, launch_gated_norm_bwd(p.dtype, d, b, in, a->dy, a->dz, s));
@@ -283,7 +291,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   SSD_PHASE(tm, SSD_PH_BWD_PASS,
             launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
                                   d.has_init ? a->dinit : nullptr, s));
-  if (p.fused_bwd) {
+  if (fused) {
     // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
     SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_main(d, b, in, dY, a->dx, s));
     SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_bc(d, b, in, a->dB, a->dC, s));
@@ -294,7 +302,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   SSD_PHASE(tm, SSD_PH_BWD_FINISH,
             launch_bwd_finish(p.dtype, d, b, in, d.has_dt ? a->ddt : nullptr,
                               d.a_mode == SSD_A_PER_TOKEN ? a->dA : nullptr, s));
-  if (p.nslices > 1 && !p.fused_bwd) {
+  if (p.nslices > 1 && !fused) {
     const int64_t nelem = d.R * d.G * d.N;
     SSD_TRY(tm.begin(SSD_PH_BWD_REDUCE_BC));
     SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dB_part, a->dB, s));

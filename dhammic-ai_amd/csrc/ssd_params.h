@@ -31,6 +31,7 @@ struct SsdBufs {
   // backward scratch
   void* dyp;               // [R][H][P] (T) gradient at y before the gated norm (has_z)
   float* dst;              // [max_chunks][H][Ppad][Npad] local dh, then gradient leaving each chunk
+  bf16* dst16;             // fused path: the gradient leaving each chunk in bf16 (dst keeps the local dh)
   float* dtot_part;        // [max_chunks][H][npass_blk]
   float* rowG;             // [nrowg][max_chunks][H][Qpad] (partials summed by the finish kernel)
   float* colG;             // [max_chunks][H][Qpad]

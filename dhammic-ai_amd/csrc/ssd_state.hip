@@ -138,6 +138,8 @@ __global__ void __launch_bounds__(SSD_PASS_THREADS) k_state_pass_fwd(SsdDims d, 
 // ---------------------------------------------------------------------------
 // Reverse recurrence: gradient of the state leaving chunk c is
 //   dst[c] = run;  run = exp(clamp(total_c)) * run + dh_local[c]
+// written in place over dh_local, or in bf16 to dst16 when given (the fused
+// backward reads it only as an MFMA operand).
 // from dfinal (or 0); dinit = run at the start. Also the gradient of each
 // chunk total, sum_{p,n} dst[c] * exp(total_c) * hin[c] (strict clamp mask),
 // reduced per block into dtot_part (deterministic order).
@@ -146,7 +148,8 @@ template <typename T, typename S>
 __global__ void __launch_bounds__(SSD_PASS_THREADS) k_state_pass_bwd(SsdDims d, const int32_t* __restrict__ seq_chunk0,
                                                                      const float* __restrict__ cs, float* __restrict__ buf,
                                                                      const T* __restrict__ hin, const S* __restrict__ dfin,
-                                                                     S* __restrict__ dinit, float* __restrict__ dtot_part) {
+                                                                     S* __restrict__ dinit, float* __restrict__ dtot_part,
+                                                                     bf16* __restrict__ dst16) {
   __shared__ float red[SSD_PASS_THREADS / 64];
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   const int h = blockIdx.y, sq = blockIdx.z;
@@ -166,7 +169,8 @@ __global__ void __launch_bounds__(SSD_PASS_THREADS) k_state_pass_bwd(SsdDims d, 
     float dhl = 0.0f;
     if (inside) {
       dhl = buf[off];
-      buf[off] = run;
+      if (dst16) dst16[off] = (bf16)run;
+      else buf[off] = run;
       contrib = run * dec * to_f(hin[off]) * clamp_pass(tot);
     }
     // block reduction of contrib (wave shuffle, then the 4 wave sums in order)
@@ -212,11 +216,11 @@ static hipError_t pass_bwd_t(int state_dtype, const SsdDims& d, const SsdBufs& b
   if (state_dtype == 1)
     hipLaunchKernelGGL((k_state_pass_bwd<T, bf16>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
                        b.dst, reinterpret_cast<const T*>(b.hin), reinterpret_cast<const bf16*>(dfin),
-                       reinterpret_cast<bf16*>(dinit), b.dtot_part);
+                       reinterpret_cast<bf16*>(dinit), b.dtot_part, b.dst16);
   else
     hipLaunchKernelGGL((k_state_pass_bwd<T, float>), grid, dim3(SSD_PASS_THREADS), 0, s, d, b.seq_chunk0, b.cs,
                        b.dst, reinterpret_cast<const T*>(b.hin), reinterpret_cast<const float*>(dfin),
-                       reinterpret_cast<float*>(dinit), b.dtot_part);
+                       reinterpret_cast<float*>(dinit), b.dtot_part, b.dst16);
   return hipGetLastError();
 }
 

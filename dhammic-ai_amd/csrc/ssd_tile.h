@@ -1,13 +1,11 @@
 // bf16 LDS tiles and MFMA operand access for gfx950 (wave64).
 //
 // A tile is ROWS x W bf16 (W = 32, 64 or 128 elements per row), stored row
-// after row with no padding; inside a row the 16-byte chunks are permuted by
-// an XOR with a per-row value, so that
-//   * eight consecutive rows read at the same column chunk (the k-contiguous
-//     operand read of v_mfma_f32_32x32x16_bf16) hit eight different bank
-//     groups, and
-//   * four consecutive rows read as 32 contiguous bytes each (one 16-lane
-//     group of ds_read_b64_tr_b16) hit four different bank-group pairs.
+// after row with a pitch of W + 8 elements: consecutive rows start 16 bytes
+// apart in the bank space, so eight consecutive rows read at the same column
+// chunk (the k-contiguous operand read of v_mfma_f32_32x32x16_bf16) hit eight
+// different bank groups. Every address is a per-lane row offset plus a
+// compile-time or wave-uniform part.
 //
 // Operand conventions of v_mfma_f32_32x32x16_bf16 (used throughout):
 //   A[i][k]: lane L supplies i = L % 32, k = 8 * (L / 32) + t, t = 0..7
@@ -27,16 +25,18 @@ typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 template <int W>
-__device__ __forceinline__ int tswz(int r) {
+__host__ __device__ constexpr int tpitch() {
   static_assert(W == 32 || W == 64 || W == 128, "tile width");
-  if constexpr (W == 32) return (((r >> 1) & 1) << 1) | ((r >> 2) & 1);
-  else return ((r & 3) << 1) | ((r >> 2) & 1);
+  return W + 8;
 }
+// Elements of a ROWS x W tile.
+template <int ROWS, int W>
+__host__ __device__ constexpr int tsize() { return ROWS * tpitch<W>(); }
 
 // Element offset of (row r, column k) in a W-wide tile.
 template <int W>
 __device__ __forceinline__ int toff(int r, int k) {
-  return r * W + ((((k >> 3) ^ tswz<W>(r))) << 3) + (k & 7);
+  return r * tpitch<W>() + k;
 }
 
 // Eight consecutive columns k .. k+7 (k % 8 == 0) of row r.
@@ -51,10 +51,19 @@ __device__ __forceinline__ bf16x4 tld4(const bf16* t, int r, int k) {
   return *reinterpret_cast<const bf16x4*>(t + toff<W>(r, k));
 }
 
-// Rows kb .. kb+3 of column m0 + (lane % 16) (m0 % 16 == 0, kb % 4 == 0).
+// The lane id as a value the compiler cannot treat as loop-invariant: address
+// arithmetic derived from it is recomputed where used instead of being hoisted
+// out of long loops (and kept live in registers across them).
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
+
+// Rows kb .. kb+3 of column m0 + (L % 16) (m0 % 16 == 0, kb % 4 == 0); L = lane id.
 template <int W>
-__device__ __forceinline__ bf16x4 ttr4(const bf16* t, int kb, int m0) {
-  const int q = threadIdx.x & 15;
+__device__ __forceinline__ bf16x4 ttr4(const bf16* t, int kb, int m0, int L) {
+  const int q = L & 15;
   const bf16* p = t + toff<W>(kb + (q >> 2), m0 + ((q & 3) << 2));
   const shortx4 v =
       __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
@@ -69,10 +78,10 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 // j = mbase + lane % 32), k = k0 + 8 * (lane / 32) + t, read from a tile whose
 // row index is k and column index is i (or j).
 template <int W>
-__device__ __forceinline__ bf16x8 ttr_std(const bf16* t, int k0, int mbase) {
-  const int L = threadIdx.x & 63, h = L >> 5;
+__device__ __forceinline__ bf16x8 ttr_std(const bf16* t, int k0, int mbase, int L) {
+  const int h = L >> 5;
   const int m0 = mbase + (((L >> 4) & 1) << 4);
-  return cat8(ttr4<W>(t, k0 + 8 * h, m0), ttr4<W>(t, k0 + 8 * h + 4, m0));
+  return cat8(ttr4<W>(t, k0 + 8 * h, m0, L), ttr4<W>(t, k0 + 8 * h + 4, m0, L));
 }
 
 // Operand partner of an accumulator tile reused in place (see acc_frag): for
@@ -80,10 +89,10 @@ __device__ __forceinline__ bf16x8 ttr_std(const bf16* t, int k0, int mbase) {
 // k0 + 16 kk + 8 (t / 4) + 4 (L / 32) + t % 4, the order in which the
 // accumulator registers 8 kk .. 8 kk + 7 hold them.
 template <int W>
-__device__ __forceinline__ bf16x8 ttr_perm(const bf16* t, int k0, int kk, int mbase) {
-  const int L = threadIdx.x & 63, h = L >> 5;
+__device__ __forceinline__ bf16x8 ttr_perm(const bf16* t, int k0, int kk, int mbase, int L) {
+  const int h = L >> 5;
   const int m0 = mbase + (((L >> 4) & 1) << 4);
-  return cat8(ttr4<W>(t, k0 + 16 * kk + 4 * h, m0), ttr4<W>(t, k0 + 16 * kk + 8 + 4 * h, m0));
+  return cat8(ttr4<W>(t, k0 + 16 * kk + 4 * h, m0, L), ttr4<W>(t, k0 + 16 * kk + 8 + 4 * h, m0, L));
 }
 
 // Registers 8 kk .. 8 kk + 7 of an accumulator tile X, as bf16: used as the B
@@ -150,6 +159,26 @@ __device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, 
   }
 }
 
+// Vector-only variant: 16-byte loads are valid (row stride and column offset
+// multiples of 8 elements, width a multiple of 8, 16-byte aligned base).
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_load_v(TileStage<ROWS, W, NTHR>& s, const bf16* __restrict__ g, int64_t ld,
+                                              int nrows, int width) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (bf16)0.0f;
+      if (r < nrows && k < width) v = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + k);
+      s.v[q] = v;
+    }
+  }
+}
+
 // Same, from an fp32 row-major source (converted to bf16); rows of `ld` floats,
 // 16-byte aligned rows (ld % 4 == 0, W <= ld).
 template <int ROWS, int W, int NTHR>
@@ -181,9 +210,8 @@ __device__ __forceinline__ float clamp_med3(float v, float lo, float hi) { retur
 #define SSD_T2 (20.0f * SSD_LOG2E)
 
 // Sum of v over the 32 lanes of each half-wave, for 16 values at once.
-// Afterwards lane L holds, in out, the sum of v[(L >> 1) & 15] over its half.
-__device__ __forceinline__ float half_reduce16(float (&v)[16]) {
-  const int L = threadIdx.x & 63;
+// Afterwards lane L returns the sum of v[(L >> 1) & 15] over its half.
+__device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
   float a[8];
   {
     const bool b = (L >> 4) & 1;
