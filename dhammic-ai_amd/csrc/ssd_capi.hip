@@ -90,7 +90,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->hslice = (d.hpg + ns - 1) / ns;
   p->nslices = (d.hpg + p->hslice - 1) / p->hslice;
   p->npass_blk = ((int64_t)d.Ppad * d.Npad + SSD_PASS_THREADS - 1) / SSD_PASS_THREADS;
-  p->norm_blocks = R < 1024 ? R : 1024;
+  p->norm_blocks = R < 512 ? R : 512;
 
   const size_t es = p->dtype == SSD_DTYPE_BF16 ? 2 : 4;
   const size_t MC = (size_t)max_chunks, H = (size_t)d.H, PN = (size_t)d.Ppad * d.Npad;
@@ -246,10 +246,16 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
   SSD_PHASE(tm, SSD_PH_CHUNK_TABLE, launch_chunk_table(d, b, a->cu_seqlens, s));
   SSD_PHASE(tm, SSD_PH_CUMSUM,
             launch_chunk_cumsum(p.dtype, d, b, a->A, a->dt, desc->want_A_cumsum ? a->A_cumsum_out : nullptr, s));
-  SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, a->dt, b.st, s));
-  SSD_PHASE(tm, SSD_PH_FWD_PASS,
-            launch_state_pass_fwd(p.dtype, p.state_dtype, d, b, d.has_init ? a->init : nullptr,
-                                  desc->want_final ? a->final_state : nullptr, s));
+  if (state_fused_supported(p.dtype, d)) {
+    SSD_PHASE(tm, SSD_PH_FWD_PASS,
+              launch_state_fwd_fused(d, b, a->x, a->B, a->dt, d.has_init ? a->init : nullptr,
+                                     desc->want_final ? a->final_state : nullptr, p.state_dtype, s));
+  } else {
+    SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, a->dt, b.st, s));
+    SSD_PHASE(tm, SSD_PH_FWD_PASS,
+              launch_state_pass_fwd(p.dtype, p.state_dtype, d, b, d.has_init ? a->init : nullptr,
+                                    desc->want_final ? a->final_state : nullptr, s));
+  }
   SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, d.has_z ? b.ypre : a->y, s));
   if (d.has_z) SSD_PHASE(tm, SSD_PH_NORM_FWD, launch_gated_norm_fwd(p.dtype, d, b, in, a->y, s));
   return SSD_OK;
@@ -287,10 +293,17 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
       SSD_PHASE(tm, SSD_PH_NORM_DW, launch_reduce_rows((int)p.norm_blocks, d.H * d.P, b.dw_part, a->dnorm_weight, s));
     dY = b.dyp;
   }
-  SSD_PHASE(tm, SSD_PH_BWD_STATE, launch_chunk_state(p.dtype, 1, d, b, dY, a->C, a->dt, b.dst, s));
-  SSD_PHASE(tm, SSD_PH_BWD_PASS,
-            launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
-                                  d.has_init ? a->dinit : nullptr, s));
+  if (fused && state_fused_supported(p.dtype, d)) {
+    b.npass_blk = state_fused_slices(d);  // dtot partials: one per headdim slice
+    SSD_PHASE(tm, SSD_PH_BWD_PASS,
+              launch_state_bwd_fused(d, b, dY, a->C, d.has_dfinal ? a->dfinal : nullptr,
+                                     d.has_init ? a->dinit : nullptr, p.state_dtype, s));
+  } else {
+    SSD_PHASE(tm, SSD_PH_BWD_STATE, launch_chunk_state(p.dtype, 1, d, b, dY, a->C, a->dt, b.dst, s));
+    SSD_PHASE(tm, SSD_PH_BWD_PASS,
+              launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
+                                    d.has_init ? a->dinit : nullptr, s));
+  }
   if (fused) {
     // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
     SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_main(d, b, in, dY, a->dx, s));

@@ -65,23 +65,27 @@ hipError_t launch_reduce_heads(const SsdDims& d, const SsdBufs& b, float* dA_hea
   return hipGetLastError();
 }
 
-// out[k] = sum_b part[b][k]: block of 256 threads = 64 columns x 4 row groups;
-// row group g sums rows g, g + 4, ... in order, then the four group sums are
-// added in order (deterministic).
-__global__ void __launch_bounds__(256) k_reduce_rows(int nblocks, int width, const float* __restrict__ part,
-                                                     float* __restrict__ out) {
-  __shared__ float red[4][64];
+// out[k] = sum_b part[b][k]: block of 1024 threads = 64 columns x 16 row
+// groups; row group g sums rows g, g + 16, ... in order, then the group sums
+// are added in a fixed tree order (deterministic).
+__global__ void __launch_bounds__(1024) k_reduce_rows(int nblocks, int width, const float* __restrict__ part,
+                                                      float* __restrict__ out) {
+  __shared__ float red[16][64];
   const int col = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + col;
   float acc = 0.0f;
   if (k < width)
-    for (int b = grp; b < nblocks; b += 4) acc += part[(int64_t)b * width + k];
+    for (int b = grp; b < nblocks; b += 16) acc += part[(int64_t)b * width + k];
   red[grp][col] = acc;
   __syncthreads();
-  if (grp == 0 && k < width) out[k] = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
+  for (int o = 8; o > 0; o >>= 1) {
+    if (grp < o) red[grp][col] += red[grp + o][col];
+    __syncthreads();
+  }
+  if (grp == 0 && k < width) out[k] = red[0][col];
 }
 
 hipError_t launch_reduce_rows(int nblocks, int width, const float* part, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(k_reduce_rows, dim3((width + 63) / 64), dim3(256), 0, s, nblocks, width, part, out);
+  hipLaunchKernelGGL(k_reduce_rows, dim3((width + 63) / 64), dim3(1024), 0, s, nblocks, width, part, out);
   return hipGetLastError();
 }
