@@ -68,7 +68,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->dtype = s->dtype;
   p->state_dtype = s->state_dtype;
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
-  if (lds_chunk_scan_fwd(p->dtype, d) > kMaxLds ||
+  if ((scan_fwd_chunk_supported(p->dtype, d) ? lds_scan_fwd_chunk(d) : lds_chunk_scan_fwd(p->dtype, d)) > kMaxLds ||
       (p->fused_bwd ? lds_bwd_main(d) > kMaxLds
                     : (lds_bwd_col(p->dtype, d) > kMaxLds || lds_bwd_row(p->dtype, d) > kMaxLds)))
     return SSD_ERR_UNSUPPORTED;
@@ -256,7 +256,11 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
               launch_state_pass_fwd(p.dtype, p.state_dtype, d, b, d.has_init ? a->init : nullptr,
                                     desc->want_final ? a->final_state : nullptr, s));
   }
-  SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, d.has_z ? b.ypre : a->y, s));
+  void* yout = d.has_z ? b.ypre : a->y;
+  if (scan_fwd_chunk_supported(p.dtype, d) && d.vec_x && d.vec_bc)
+    SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_scan_fwd_chunk(d, b, in, yout, s));
+  else
+    SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, yout, s));
   if (d.has_z) SSD_PHASE(tm, SSD_PH_NORM_FWD, launch_gated_norm_fwd(p.dtype, d, b, in, a->y, s));
   return SSD_OK;
 }

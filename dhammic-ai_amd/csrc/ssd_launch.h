@@ -49,6 +49,11 @@ hipError_t launch_state_fwd_fused(const SsdDims& d, const SsdBufs& b, const void
 hipError_t launch_state_bwd_fused(const SsdDims& d, const SsdBufs& b, const void* dy, const void* C,
                                   const void* dfinal, void* dinit, int state_dtype, hipStream_t s);
 
+// ssd_scan_fwd_chunk.hip (bf16 with 16-byte vector access): one block per (chunk, head slice)
+bool scan_fwd_chunk_supported(int dtype, const SsdDims& d);
+size_t lds_scan_fwd_chunk(const SsdDims& d);
+hipError_t launch_scan_fwd_chunk(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s);
+
 // ssd_scan_fwd.hip
 hipError_t launch_chunk_scan_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
                                  void* y, hipStream_t s);
