@@ -165,45 +165,48 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     zero(dCoT[ntk]);
   }
 
+  // Inputs of the tile phase (x, dy, cs, dt) are loaded during the previous
+  // head's state phase; those of the state phase (dst, h_in) during this
+  // head's tile phase.
+  struct HeadStage {
+    TileStage<64, PP, 256> x, y[kMaxSlots];
+    float cs, dt;
+  } hs;
+  auto load_tiles = [&](int h) {
+    const int l0 = threadIdx.x;
+    hs.cs = 0.0f;
+    hs.dt = 1.0f;
+    if (l0 < Qpad) {
+      hs.cs = a.cs[((int64_t)c * d.H + h) * Qpad + l0];
+      if (d.has_dt && l0 < ci.len) hs.dt = a.dt[(int64_t)(ci.row0 + l0) * d.H + h];
+    }
+    tstage_load_v(hs.x, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + (int64_t)h * d.P, xrow, min(64, ci.len - 64 * j),
+                  d.P);
+#pragma unroll
+    for (int t = 0; t < kMaxSlots; ++t)
+      if (t < nt_i)
+        tstage_load_v(hs.y[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + (int64_t)h * d.P, xrow,
+                      min(64, ci.len - 64 * (j + t)), d.P);
+  };
+  load_tiles(h_lo);
   for (int h = h_lo; h < h_hi; ++h) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
-    {
-      // every global load of the head is issued before the first LDS store
-      const float* csc = a.cs + ((int64_t)c * d.H + h) * Qpad;
-      const int l0 = threadIdx.x;
-      float csv = 0.0f, dtv = 1.0f;
-      if (l0 < Qpad) {
-        csv = csc[l0];
-        if (d.has_dt && l0 < ci.len) dtv = a.dt[(int64_t)(ci.row0 + l0) * d.H + h];
-      }
-      TileStage<64, PP, 256> sx;
-      tstage_load_v(sx, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + (int64_t)h * d.P, xrow,
-                    min(64, ci.len - 64 * j), d.P);
-      TileStage<64, PP, 256> sy[kMaxSlots];
-#pragma unroll
-      for (int t = 0; t < kMaxSlots; ++t)
-        if (t < nt_i)
-          tstage_load_v(sy[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + (int64_t)h * d.P, xrow,
-                        min(64, ci.len - 64 * (j + t)), d.P);
-      TileStage<PP, NP, 256> sd, sh;
-      tstage_load_v(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
-      tstage_load_v(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
-      __syncthreads();  // the previous head's LDS reads are done
-      if (l0 < Qpad) {
-        s_cs2[l0] = csv * SSD_LOG2E;
-        s_dt[l0] = dtv;
-      }
-      for (int e = threadIdx.x; e < 4 * 2 * 64; e += 256) red_row[e] = 0.0f;
-      tstage_store(sx, xj);
-#pragma unroll
-      for (int t = 0; t < kMaxSlots; ++t)
-        if (t < nt_i) tstage_store(sy[t], dYt + (j + t) * XT);
-      tstage_store(sd, dstT);
-      tstage_store(sh, hinT);
+    __syncthreads();  // the previous head's LDS reads are done
+    if (threadIdx.x < Qpad) {
+      s_cs2[threadIdx.x] = hs.cs * SSD_LOG2E;
+      s_dt[threadIdx.x] = hs.dt;
     }
+    for (int e = threadIdx.x; e < 4 * 2 * 64; e += 256) red_row[e] = 0.0f;
+    tstage_store(hs.x, xj);
+#pragma unroll
+    for (int t = 0; t < kMaxSlots; ++t)
+      if (t < nt_i) tstage_store(hs.y[t], dYt + (j + t) * XT);
     __syncthreads();
+    TileStage<PP, NP, 256> sd, sh;
+    tstage_load_v(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    tstage_load_v(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
 
     const float cs_last = s_cs2[Qpad - 1];
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
@@ -300,6 +303,10 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       const int sg = 64 * j + threadIdx.x;
       if (sg < ci.len) a.colG[((int64_t)c * d.H + h) * Qpad + sg] = red_col[threadIdx.x] + red_col[64 + threadIdx.x];
     }
+    tstage_store(sd, dstT);
+    tstage_store(sh, hinT);
+    __syncthreads();
+    if (h + 1 < h_hi) load_tiles(h + 1);
 
     // ---- per-token state terms of column block j (lane = token t_loc) ----
     const float cs_t = s_cs2[tg];
