@@ -350,27 +350,41 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     esum += __shfl_xor(esum, 32, 64);
     xsum += __shfl_xor(xsum, 32, 64);
 
-    // dB state part: dBs^T[n][s] += w_s dt_s sum_p dst[p][n] x[s][p]
-    // dC Y_off part: dCo^T[n][l] += e^{cs_l} sum_p h_in[p][n] dy[l][p]; dcs_off
+    // dB state part: dBs^T[n][s] += sum_p dst[p][n] (w_s dt_s x[s][p])
+    // dC Y_off part: dCo^T[n][l] += sum_p h_in[p][n] (e^{cs_l} dy[l][p]); dcs_off
+    // The per-token factors are folded into the token-side operand, so both
+    // accumulators are updated by MFMA only; dcs_off needs the unscaled
+    // product h_in dy^T per head (tc).
     const float el = t_ok ? exp2_fast(clamp_med3(cs_t, -SSD_T2, SSD_T2)) : 0.0f;
     const float pl = fabsf(cs_t) < SSD_T2 ? 1.0f : 0.0f;
+    const float wsd = ws * dts;
     float osum = 0.0f;
     const bf16* crow = a.Cm + (int64_t)(ci.row0 + (t_ok ? tg : 0)) * brow + (int64_t)g * d.N;
+    bf16x8 xs[PP / 16], ys[PP / 16], yr[PP / 16];
+#pragma unroll
+    for (int kq = 0; kq < PP / 16; ++kq) {
+      const bf16x8 xb = tld8<PP>(xj, t_loc, 16 * kq + 8 * hh);
+      yr[kq] = tld8<PP>(dyc, t_loc, 16 * kq + 8 * hh);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xs[kq][e] = (bf16)((float)xb[e] * wsd);
+        ys[kq][e] = (bf16)((float)yr[kq][e] * el);
+      }
+    }
 #pragma unroll
     for (int ntk = 0; ntk < NTW; ++ntk) {
       const int nt = 2 * ntk + wc;
       if (nt >= NT) continue;
-      floatx16 tb, tc;
-      zero(tb);
+      floatx16 tc;
       zero(tc);
 #pragma unroll
-      for (int kk = 0; kk < PP; kk += 16) {
-        const bf16x8 xb = tld8<PP>(xj, t_loc, kk + 8 * hh);
-        const bf16x8 yb = tld8<PP>(dyc, t_loc, kk + 8 * hh);
-        mfma(tb, ttr_std<NP>(dstT, kk, 32 * nt, lane), xb);
-        mfma(tc, ttr_std<NP>(hinT, kk, 32 * nt, lane), yb);
+      for (int kq = 0; kq < PP / 16; ++kq) {
+        const bf16x8 dA = ttr_std<NP>(dstT, 16 * kq, 32 * nt, lane);
+        const bf16x8 hA = ttr_std<NP>(hinT, 16 * kq, 32 * nt, lane);
+        mfma(dBT[ntk], dA, xs[kq]);
+        mfma(dCoT[ntk], hA, ys[kq]);
+        mfma(tc, hA, yr[kq]);
       }
-      const float wsd = ws * dts;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n0 = 32 * nt + 8 * r + 4 * hh;
@@ -379,15 +393,10 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
         for (int e = 0; e < 4; ++e) cq[e] = (bf16)0.0f;
         if (t_ok && n0 < d.N) cq = *reinterpret_cast<const bf16x4*>(crow + n0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * r + e;
-          dBT[ntk][v] = fmaf(tb[v], wsd, dBT[ntk][v]);
-          const float tcv = tc[v] * el;
-          dCoT[ntk][v] += tcv;
-          osum += tcv * (float)cq[e];
-        }
+        for (int e = 0; e < 4; ++e) osum += tc[4 * r + e] * (float)cq[e];
       }
     }
+    osum *= el;
     osum += __shfl_xor(osum, 32, 64);
     for (int o = 32; o > 0; o >>= 1) dpart += __shfl_xor(dpart, o, 64);
     if (hh == 0) {
