@@ -18,8 +18,9 @@
 // (same block index mod 8) so their shared x / dy rows are read from HBM once.
 // Tokens are staged 64 at a time (x or dy rows, B or C columns scaled per
 // token) and both MFMA operands are read with ds_read_b64_tr_b16 (the
-// contraction is over tokens, the tiles' row index). The next 64 tokens are
-// loaded into registers while the current ones compute.
+// contraction is over tokens, the tiles' row index; the tiles use the
+// transpose-read pitch). Global loads run three 64-token steps ahead through a
+// ring of three register stages.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
 
@@ -43,7 +44,7 @@ __device__ __forceinline__ void state_load(StateStage<PT>& st, const bf16* U, co
 template <int PT>
 __device__ __forceinline__ void state_store(const StateStage<PT>& st, bf16* tu, bf16* tv, const float* coef) {
   constexpr int NTHR = StateStage<PT>::NTHR;
-  tstage_store(st.u, tu);
+  tstage_store<64, 32 * PT, NTHR, tpitch_tr<32 * PT>()>(st.u, tu);
 #pragma unroll
   for (int q = 0; q < TileStage<64, 32, NTHR>::PER; ++q) {
     const int id = threadIdx.x + q * NTHR;
@@ -53,27 +54,30 @@ __device__ __forceinline__ void state_store(const StateStage<PT>& st, bf16* tu, 
       bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)st.v.v[q][e] * sc);
-      *reinterpret_cast<bf16x8*>(tv + toff<32>(r, k)) = o;
+      *reinterpret_cast<bf16x8*>(tv + toff<32, tpitch_tr<32>()>(r, k)) = o;
     }
   }
 }
 
-// Per-token coefficient inputs of one 64-token step (threads < 64: token t0 + tid).
+// Scalars of one 64-token step: its chunk's row range and total log-decay, and
+// the per-token inputs of the coefficients (threads < 64: token t0 + tid).
 struct StepCoef {
-  float cs_tok, dt_tok;
+  float cs_tok, dt_tok, tot;
+  int row0, len;
 };
 
 template <int PT, bool FWD>
-__global__ void __launch_bounds__(64 * PT) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2, 2))) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
                                                          const float* __restrict__ cs, const float* __restrict__ dt,
                                                          const bf16* __restrict__ U, const bf16* __restrict__ V,
                                                          bf16* __restrict__ hst, const bf16* __restrict__ hin_in,
                                                          const void* __restrict__ s_in, void* __restrict__ s_out,
                                                          int state_bf16, float* __restrict__ dtot_part) {
-  constexpr int PP = 32 * PT, NTHR = 64 * PT;
-  __shared__ __align__(16) bf16 tu[2][tsize<64, PP>()];
-  __shared__ __align__(16) bf16 tv[2][tsize<64, 32>()];
+  constexpr int PP = 32 * PT;
+  constexpr int UPI = tpitch_tr<PP>(), VPI = tpitch_tr<32>();
+  __shared__ __align__(16) bf16 tu[2][tsize<64, PP, UPI>()];
+  __shared__ __align__(16) bf16 tv[2][tsize<64, 32, VPI>()];
   __shared__ float coef[2][64];
   __shared__ float red[4];
   // block -> (n tile, unit = (head, sequence)); the n tiles of a unit share an XCD
@@ -107,34 +111,42 @@ __global__ void __launch_bounds__(64 * PT) k_state_fused(SsdDims d, const ChunkI
   }
   const int c0 = seq_chunk0[sq], c1 = seq_chunk0[sq + 1];
   const int nch = c1 - c0;
-  // flat walk over (chunk k, 64-token step t0); everything a step needs from
-  // global memory is loaded one step ahead
   auto chunk_of = [&](int k) { return FWD ? c0 + k : c1 - 1 - k; };
-  auto load_step = [&](StateStage<PT>& st, StepCoef& cf, int k, int t0) {
-    const int c = chunk_of(k);
+
+  // load cursor (kl, tl): the next step whose inputs are fetched
+  int kl = 0, tl = 0;
+  auto load_next = [&](StateStage<PT>& st, StepCoef& cf) {
+    if (kl >= nch) return;
+    const int c = chunk_of(kl);
     const ChunkInfo ci = chunks[c];
-    state_load<PT>(st, U, V, urow, vrow, ci.row0, t0, ci.len, d.P, nw, ucol, vcol);
+    state_load<PT>(st, U, V, urow, vrow, ci.row0, tl, ci.len, d.P, nw, ucol, vcol);
+    cf.row0 = ci.row0;
+    cf.len = ci.len;
+    cf.tot = cs[((int64_t)c * d.H + h) * d.Qpad + d.Qpad - 1];
     cf.cs_tok = 0.0f;
     cf.dt_tok = 1.0f;
     if (threadIdx.x < 64) {
-      const int l = t0 + threadIdx.x;
+      const int l = tl + threadIdx.x;
       cf.cs_tok = cs[((int64_t)c * d.H + h) * d.Qpad + min(l, d.Qpad - 1)];
       if (FWD && d.has_dt && l < ci.len) cf.dt_tok = dt[(int64_t)(ci.row0 + l) * d.H + h];
     }
+    tl += 64;
+    if (tl >= ci.len) {
+      ++kl;
+      tl = 0;
+    }
   };
 
-  StateStage<PT> st;
-  StepCoef cf;
-  int k = 0, t0 = 0;
-  if (nch > 0) load_step(st, cf, 0, 0);
+  // compute cursor (k, t0)
+  int k = 0, t0 = 0, buf = 0;
   floatx16 acc;
   zero(acc);
   bf16 hin_v[16];
-  int buf = 0;
-  while (k < nch) {
+  // one 64-token step on the inputs in (st, cf); refills them with the step three ahead
+  auto step = [&](StateStage<PT>& st, StepCoef& cf) {
     const int c = chunk_of(k);
-    const ChunkInfo ci = chunks[c];
-    const float tot = cs[((int64_t)c * d.H + h) * d.Qpad + d.Qpad - 1];
+    const int clen = cf.len;
+    const float tot = cf.tot;
     const int64_t soff = ((int64_t)c * d.H + h) * d.Ppad * d.Npad;
     if (t0 == 0) {
       // state entering (forward) / gradient leaving (backward) chunk c
@@ -145,28 +157,22 @@ __global__ void __launch_bounds__(64 * PT) k_state_fused(SsdDims d, const ChunkI
         if (!FWD) hin_v[v] = hin_in[o];  // consumed at the end of the chunk
       }
     }
-    // per-token coefficient of the V rows
     if (threadIdx.x < 64) {
       const int l = t0 + threadIdx.x;
       float v = 0.0f;
-      if (l < ci.len) v = FWD ? exp_clamp(tot - cf.cs_tok) * cf.dt_tok : exp_clamp(cf.cs_tok);
+      if (l < clen) v = FWD ? exp_clamp(tot - cf.cs_tok) * cf.dt_tok : exp_clamp(cf.cs_tok);
       coef[buf][threadIdx.x] = v;
     }
     __syncthreads();  // coef visible; this buffer's previous readers are done
     state_store<PT>(st, tu[buf], tv[buf], coef[buf]);
     __syncthreads();
-    // next step
-    int k2 = k, t2 = t0 + 64;
-    if (t2 >= ci.len) {
-      k2 = k + 1;
-      t2 = 0;
-    }
-    if (k2 < nch) load_step(st, cf, k2, t2);
+    load_next(st, cf);  // st / cf are free now: refill with the step three ahead
 #pragma unroll
     for (int kk = 0; kk < 64; kk += 16)
-      mfma(acc, ttr_std<PP>(tu[buf], kk, prow0, lane), ttr_std<32>(tv[buf], kk, 0, lane));
+      mfma(acc, ttr_std<PP, UPI>(tu[buf], kk, prow0, lane), ttr_std<32, VPI>(tv[buf], kk, 0, lane));
     buf ^= 1;
-    if (k2 != k) {
+    t0 += 64;
+    if (t0 >= clen) {
       // end of chunk c
       const float dec = exp_clamp(tot);
       if (!FWD) {
@@ -186,9 +192,22 @@ __global__ void __launch_bounds__(64 * PT) k_state_fused(SsdDims d, const ChunkI
 #pragma unroll
       for (int v = 0; v < 16; ++v) run[v] = dec * run[v] + acc[v];
       zero(acc);
+      ++k;
+      t0 = 0;
     }
-    k = k2;
-    t0 = t2;
+  };
+
+  StateStage<PT> st0, st1, st2;
+  StepCoef cf0, cf1, cf2;
+  load_next(st0, cf0);
+  load_next(st1, cf1);
+  load_next(st2, cf2);
+  while (k < nch) {
+    step(st0, cf0);
+    if (k >= nch) break;
+    step(st1, cf1);
+    if (k >= nch) break;
+    step(st2, cf2);
   }
   // final state (forward) / gradient of the initial state (backward)
   if (s_out) {

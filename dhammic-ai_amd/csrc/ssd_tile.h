@@ -1,10 +1,13 @@
 // bf16 LDS tiles and MFMA operand access for gfx950 (wave64).
 //
 // A tile is ROWS x W bf16 (W = 32, 64 or 128 elements per row), stored row
-// after row with a pitch of W + 8 elements: consecutive rows start 16 bytes
-// apart in the bank space, so eight consecutive rows read at the same column
-// chunk (the k-contiguous operand read of v_mfma_f32_32x32x16_bf16) hit eight
-// different bank groups. Every address is a per-lane row offset plus a
+// after row with a pitch of PI elements. The default PI = W + 8 starts
+// consecutive rows 16 bytes apart in the bank space, so eight consecutive rows
+// read at the same column chunk (the k-contiguous operand read of
+// v_mfma_f32_32x32x16_bf16) hit eight different bank groups. Tiles read only
+// through ds_read_b64_tr_b16 (four consecutive rows, 32 bytes each) use
+// PI = W + 16 instead: rows then start 32 bytes apart modulo 128 and the four
+// rows never share a bank. Every address is a per-lane row offset plus a
 // compile-time or wave-uniform part.
 //
 // Operand conventions of v_mfma_f32_32x32x16_bf16 (used throughout):
@@ -29,26 +32,32 @@ __host__ __device__ constexpr int tpitch() {
   static_assert(W == 32 || W == 64 || W == 128, "tile width");
   return W + 8;
 }
+// Pitch of a tile read only with ds_read_b64_tr_b16.
+template <int W>
+__host__ __device__ constexpr int tpitch_tr() {
+  static_assert(W == 32 || W == 64 || W == 128, "tile width");
+  return W + 16;
+}
 // Elements of a ROWS x W tile.
-template <int ROWS, int W>
-__host__ __device__ constexpr int tsize() { return ROWS * tpitch<W>(); }
+template <int ROWS, int W, int PI = tpitch<W>()>
+__host__ __device__ constexpr int tsize() { return ROWS * PI; }
 
 // Element offset of (row r, column k) in a W-wide tile.
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ int toff(int r, int k) {
-  return r * tpitch<W>() + k;
+  return r * PI + k;
 }
 
 // Eight consecutive columns k .. k+7 (k % 8 == 0) of row r.
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ bf16x8 tld8(const bf16* t, int r, int k) {
-  return *reinterpret_cast<const bf16x8*>(t + toff<W>(r, k));
+  return *reinterpret_cast<const bf16x8*>(t + toff<W, PI>(r, k));
 }
 
 // Four consecutive columns k .. k+3 (k % 4 == 0) of row r.
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ bf16x4 tld4(const bf16* t, int r, int k) {
-  return *reinterpret_cast<const bf16x4*>(t + toff<W>(r, k));
+  return *reinterpret_cast<const bf16x4*>(t + toff<W, PI>(r, k));
 }
 
 // The lane id as a value the compiler cannot treat as loop-invariant: address
@@ -61,10 +70,10 @@ __device__ __forceinline__ int opaque_lane() {
 }
 
 // Rows kb .. kb+3 of column m0 + (L % 16) (m0 % 16 == 0, kb % 4 == 0); L = lane id.
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ bf16x4 ttr4(const bf16* t, int kb, int m0, int L) {
   const int q = L & 15;
-  const bf16* p = t + toff<W>(kb + (q >> 2), m0 + ((q & 3) << 2));
+  const bf16* p = t + toff<W, PI>(kb + (q >> 2), m0 + ((q & 3) << 2));
   const shortx4 v =
       __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
   return __builtin_bit_cast(bf16x4, v);
@@ -77,22 +86,22 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 // k-contiguous operand (A[i][k] with i = mbase + lane % 32, or B[k][j] with
 // j = mbase + lane % 32), k = k0 + 8 * (lane / 32) + t, read from a tile whose
 // row index is k and column index is i (or j).
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ bf16x8 ttr_std(const bf16* t, int k0, int mbase, int L) {
   const int h = L >> 5;
   const int m0 = mbase + (((L >> 4) & 1) << 4);
-  return cat8(ttr4<W>(t, k0 + 8 * h, m0, L), ttr4<W>(t, k0 + 8 * h + 4, m0, L));
+  return cat8(ttr4<W, PI>(t, k0 + 8 * h, m0, L), ttr4<W, PI>(t, k0 + 8 * h + 4, m0, L));
 }
 
 // Operand partner of an accumulator tile reused in place (see acc_frag): for
 // MFMA step kk over the 32 rows k0 .. k0+31, lane L supplies the rows
 // k0 + 16 kk + 8 (t / 4) + 4 (L / 32) + t % 4, the order in which the
 // accumulator registers 8 kk .. 8 kk + 7 hold them.
-template <int W>
+template <int W, int PI = tpitch<W>()>
 __device__ __forceinline__ bf16x8 ttr_perm(const bf16* t, int k0, int kk, int mbase, int L) {
   const int h = L >> 5;
   const int m0 = mbase + (((L >> 4) & 1) << 4);
-  return cat8(ttr4<W>(t, k0 + 16 * kk + 4 * h, m0, L), ttr4<W>(t, k0 + 16 * kk + 8 + 4 * h, m0, L));
+  return cat8(ttr4<W, PI>(t, k0 + 16 * kk + 4 * h, m0, L), ttr4<W, PI>(t, k0 + 16 * kk + 8 + 4 * h, m0, L));
 }
 
 // Registers 8 kk .. 8 kk + 7 of an accumulator tile X, as bf16: used as the B
@@ -146,7 +155,7 @@ __device__ __forceinline__ void tstage_load(TileStage<ROWS, W, NTHR>& s, const b
   }
 }
 
-template <int ROWS, int W, int NTHR>
+template <int ROWS, int W, int NTHR, int PI = tpitch<W>()>
 __device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, bf16* t) {
   constexpr int CPR = W / 8;
 #pragma unroll
@@ -154,7 +163,7 @@ __device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, 
     const int id = threadIdx.x + q * NTHR;
     if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
       const int r = id / CPR, k = (id % CPR) * 8;
-      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = s.v[q];
+      *reinterpret_cast<bf16x8*>(t + toff<W, PI>(r, k)) = s.v[q];
     }
   }
 }
