@@ -55,31 +55,36 @@ def make_inputs(dev, seed=2):
 
 
 def phase_models(nchunks):
-    """Algorithmic FLOPs (matrix contractions, causal count, no recompute credit)
-    and logical HBM bytes (each input read once, each output written once) per
-    launch of each phase, at the bench config. Per-token FLOP terms follow the
-    fwd+bwd split F_tok = H(3(Q+1)P + 12NP) + 3G(Q+1)N."""
+    """Algorithmic FLOPs (matrix contractions, causal count, no credit for
+    recompute) and logical HBM bytes (each input of the kernel read once, each
+    output written once) per launch of each phase that runs at the bench
+    config (bf16, 16-byte aligned rows: the fused state, scan and backward
+    kernels). The per-token FLOP terms split the whole call's
+    F_tok = H(3(Q+1)P + 12NP) + 3G(Q+1)N over the kernels that compute them."""
     b, L, H, P, G, N, Q = (CFG[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate",
                                             "chunk"))
     R = b * L
     es = 2
+    nb = -(-Q // 64)
     x = R * H * P * es          # x, y, z, dy, dx, dz, y_pre, dy_pre: one bf16 (R,H,P) tensor
     bc = R * G * N * es         # B or C
     dt = R * H * 4
-    st32 = nchunks * H * P * N * 4
-    st16 = nchunks * H * P * N * es
-    cs = nchunks * H * Q * 4
+    st16 = nchunks * H * P * N * es          # hin or dst (bf16, one state per chunk and head)
+    fin = b * H * P * N * 4                  # final state / dfinal / dinit (fp32)
+    cs = nchunks * H * Q * 4                 # in-chunk cumsum, and each per-token fp32 vector
+    dS = nchunks * G * (nb * (nb + 1) // 2) * 64 * 64 * 4   # head-summed dS tiles (fp32)
+    bcp = R * G * N * 4                      # dB state part / dC Y_off part (fp32)
     m = {
-        "fwd_state": (R * H * 2 * N * P, x + bc + dt + cs + st32),
-        "fwd_pass": (0, st32 + st16 + cs),
+        "cumsum": (0, dt + cs),
+        "fwd_pass": (R * H * 2 * N * P, x + bc + dt + cs + st16 + fin),
         "fwd_scan": (R * (G * (Q + 1) * N + H * ((Q + 1) * P + 2 * N * P)), 2 * x + 2 * bc + dt + cs + st16),
         "norm_fwd": (0, 3 * x + R * 4),
         "norm_bwd": (0, 5 * x + R * 4),
-        "bwd_state": (R * H * 2 * N * P, x + bc + cs + st32),
-        "bwd_pass": (0, 2 * st32 + st16 + cs),
-        "bwd_col": (R * (H * (2 * (Q + 1) * P + 4 * N * P) + G * (Q + 1) * N),
-                    3 * x + 2 * bc + dt + cs + st32),
-        "bwd_row": (R * (H * 2 * N * P + G * (Q + 1) * N), 2 * x + 3 * bc + dt + cs + st16),
+        "bwd_pass": (R * H * 2 * N * P, x + bc + cs + 2 * st16 + 2 * fin),
+        "bwd_col": (R * H * (2 * (Q + 1) * P + 6 * N * P),
+                    3 * x + 2 * bc + dt + cs + 2 * st16 + dS + 2 * bcp + ((nb + 1) / 2 + 4) * cs),
+        "bwd_row": (R * G * 2 * (Q + 1) * N, 4 * bc + dS + 2 * bcp),
+        "bwd_finish": (0, ((nb + 1) / 2 + 5) * cs + 2 * dt),
     }
     return m
 
@@ -164,8 +169,9 @@ def time_gpu(steps, warmup, probe=False):
             except RuntimeError:
                 vals = []
                 break
-        # a phase that did not run keeps the two initial records: ~0 ms apart
-        if vals and max(vals) > 0.0005:
+        # a phase that did not run keeps its two initial records, taken before `start`
+        ran = all(start.elapsed_time(row[2 * k]) > 0.0 for row in ev)
+        if vals and ran:
             phases[name] = statistics.mean(vals)
     # the same event pairs bracket the fwd_scan / bwd kernels of every step; also
     # count chunks for the models
@@ -173,11 +179,10 @@ def time_gpu(steps, warmup, probe=False):
     return ms_total / steps, wall / steps * 1e3, phases, nchunks
 
 
-def roofline(phases, nchunks):
-    models = phase_models(nchunks)
-    name = max(phases, key=lambda k: phases[k])
+def kernel_roofline(name, ms, models):
+    """Roofline entry of one phase: HBM-bound below the ridge, MFMA-bound above."""
     flops, nbytes = models.get(name, (0, 0))
-    t_s = phases[name] * 1e-3
+    t_s = ms * 1e-3
     intensity = flops / nbytes if nbytes else 0.0
     if intensity > RIDGE:
         achieved = flops / t_s / 1e12
@@ -186,27 +191,45 @@ def roofline(phases, nchunks):
         achieved = nbytes / t_s / 1e9
         out = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     out["frac"] = out["achieved"] / out["peak"]
-    out["kernel"] = name
-    out["kernel_ms"] = phases[name]
     out["algorithmic_flops"] = flops
     out["algorithmic_bytes"] = nbytes
-    out["traffic"] = measured_traffic(name)
+    if flops:
+        out["mfma_frac"] = flops / t_s / 1e12 / PEAK_BF16_TFLOPS
     return out
+
+
+def roofline(phases, nchunks):
+    """The dominant kernel's roofline entry, and every modelled phase's."""
+    models = phase_models(nchunks)
+    name = max(phases, key=lambda k: phases[k])
+    out = kernel_roofline(name, phases[name], models)
+    out["kernel"] = name
+    out["kernel_ms"] = phases[name]
+    out["traffic"] = measured_traffic(name)
+    per = {}
+    for k, ms in phases.items():
+        if k in models:
+            e = kernel_roofline(k, ms, models)
+            per[k] = {"ms": round(ms, 4), "bound": e["bound"], "frac": round(e["frac"], 4)}
+            if "mfma_frac" in e:
+                per[k]["mfma_frac"] = round(e["mfma_frac"], 4)
+    return out, per
 
 
 def cpu_baseline():
     """The reference's chunked PyTorch path (oracle restatement of
     r2/dhammic-ai/src/kernels/ssd_scan.py:330-533), fp32, timed on host cores:
     forward under no_grad, backward = re-run forward + autograd.grad (the
-    FusedSSDScan pattern). Sample: one batch row, 8 of config 2's 64 heads,
-    L=2048 (8 chunks), P=64, N=128, Q=256; tokens/s scaled to all 64 heads."""
+    FusedSSDScan pattern). Sample: one batch row of config 2 (L=8192, 32
+    chunks), 8 of its 64 heads, P=64, N=128, Q=256, repeated for about 12 s;
+    tokens/s scaled to all 64 heads."""
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle import ssd_chunked as oc
 
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
-    b, L, Hs, P, N, Q = 1, 2048, 8, CFG["headdim"], CFG["dstate"], CFG["chunk"]
+    b, L, Hs, P, N, Q = 1, CFG["seqlen"], 8, CFG["headdim"], CFG["dstate"], CFG["chunk"]
     g = torch.Generator().manual_seed(0)
     x = torch.randn(b, L, Hs, P, generator=g)
     dt = torch.nn.functional.softplus(torch.randn(b, L, Hs, generator=g) - 4.0).clamp(1e-3, 0.1)
@@ -218,7 +241,7 @@ def cpu_baseline():
     times = []
     budget = 12.0
     t_all = time.perf_counter()
-    for i in range(2 + 30):
+    for i in range(2 + 200):
         t0 = time.perf_counter()
         oc.fused_ssd_scan_fwd_bwd_baseline(X, a, Bm, Cm, Q, dY)
         dtime = time.perf_counter() - t0
@@ -257,7 +280,7 @@ def main():
     ms_step, wall_ms, phases, nchunks = time_gpu(a.steps, a.warmup, a.copy_probe)
     tokens = CFG["batch"] * CFG["seqlen"]
     value = tokens / (ms_step * 1e-3) / 1e6
-    rl = roofline(phases, nchunks)
+    rl, per_kernel = roofline(phases, nchunks)
     out = {
         "metric": METRIC, "value": value, "unit": "Mtokens/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
@@ -266,6 +289,7 @@ def main():
                    "x_dtype": "bf16", "state_dtype": "fp32", "tokens_per_step": tokens},
         "roofline": rl,
         "kernels_ms": {k: round(v, 4) for k, v in phases.items()},
+        "kernels_roofline": per_kernel,
         "wall_ms_per_step": wall_ms,
     }
     if rank == 0 and not a.no_cpu_baseline:
