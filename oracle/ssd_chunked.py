@@ -37,7 +37,7 @@ class _Segsum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x):
         T = x.shape[-1]
-        idx = torch.arange(T)
+        idx = torch.arange(T, device=x.device)
         strict_lower = (idx[:, None] > idx[None, :]).to(x.dtype)  # [i, j] = 1 iff i > j
         # column j accumulates x[k] for k = j+1..i down the rows i
         contrib = x.unsqueeze(-1) * strict_lower                  # [..., i, j] = x[i] if i > j
@@ -52,7 +52,7 @@ class _Segsum(torch.autograd.Function):
     def backward(ctx, dy):
         (y,) = ctx.saved_tensors
         T = y.shape[-1]
-        idx = torch.arange(T)
+        idx = torch.arange(T, device=y.device)
         inside = (y > CLAMP_MIN) & (y < CLAMP_MAX)
         lower_incl = idx[:, None] >= idx[None, :]
         g = torch.where(inside & lower_incl, dy, torch.zeros_like(dy))

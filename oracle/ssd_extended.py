@@ -72,7 +72,7 @@ def ssd_combined(x, dt, A, B, C, chunk_size, D=None, z=None, norm_weight=None,
     if D is not None:
         Y = Y + x * D.view(1, 1, H, 1)
     if z is not None:
-        w = norm_weight if norm_weight is not None else torch.ones(H * P, dtype=Y.dtype)
+        w = norm_weight if norm_weight is not None else torch.ones(H * P, dtype=Y.dtype, device=Y.device)
         Y = gated_rmsnorm(Y.reshape(b, L, H * P), z.reshape(b, L, H * P), w, norm_eps)
         Y = Y.reshape(b, L, H, P)
     return Y, final
