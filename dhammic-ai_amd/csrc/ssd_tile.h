@@ -168,22 +168,43 @@ __device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Raw buffer loads: the hardware range check returns zeros for an offset at or
+// beyond the resource's size, so a masked load needs no branch. Loads issued
+// in straight-line code (no per-lane branch around them) keep their vmcnt
+// waits exact, which lets several stages of loads stay in flight.
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+#define SSD_BUF_SIZE 0x7ffffff0
+// Resource over [base, base + SSD_BUF_SIZE) bytes; base must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, SSD_BUF_SIZE, 0x00020000);
+}
+// 16 bytes at byte offset `off`, or zeros when `ok` is false.
+__device__ __forceinline__ bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, ok ? off : SSD_BUF_SIZE, 0, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+// One fp32 at byte offset `off`, or 0 when `ok` is false.
+__device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, int off, bool ok) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ok ? off : SSD_BUF_SIZE, 0, 0));
+}
+
 // Vector-only variant: 16-byte loads are valid (row stride and column offset
-// multiples of 8 elements, width a multiple of 8, 16-byte aligned base).
+// multiples of 8 elements, width a multiple of 8, 16-byte aligned base). Rows
+// >= nrows and columns >= width read as zeros through the buffer range check
+// (the tile spans less than 2 GiB from g). `g` must be wave-uniform.
 template <int ROWS, int W, int NTHR>
 __device__ __forceinline__ void tstage_load_v(TileStage<ROWS, W, NTHR>& s, const bf16* __restrict__ g, int64_t ld,
                                               int nrows, int width) {
   constexpr int CPR = W / 8;
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g);
 #pragma unroll
   for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
     const int id = threadIdx.x + q * NTHR;
     if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
       const int r = id / CPR, k = (id % CPR) * 8;
-      bf16x8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (bf16)0.0f;
-      if (r < nrows && k < width) v = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + k);
-      s.v[q] = v;
+      s.v[q] = buf_ld16(rs, (int)(((int64_t)r * ld + k) * 2), r < nrows && k < width);
     }
   }
 }
