@@ -50,7 +50,9 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
       float rg = 0.0f;
       for (int k = 0; k < bf.nrowg && k <= l / 64; ++k)
         rg += bf.rowG[(int64_t)k * d.max_chunks * d.H * d.Qpad + base + l];
-      x = rg - bf.colG[base + l] + bf.dcs_off[base + l] - bf.eterm[base + l];
+      float off = 0.0f;
+      for (int k = 0; k < bf.ndcs; ++k) off += bf.dcs_off[(int64_t)k * d.max_chunks * d.H * d.Qpad + base + l];
+      x = rg - bf.colG[base + l] + off - bf.eterm[base + l];
       esum += bf.eterm[base + l];
     }
     v[e] = x;

@@ -1,0 +1,345 @@
+// dB and dC of the chunked SSD scan backward (bf16 fused path, gfx950), and
+// the Y_off part of the decay gradient. Per chunk, 64-token block kb and
+// group g, with the head-summed dS tiles of k_bwd_main:
+//   dC_t = sum_{j <= kb} sum_s dS[t,s] B_s + sum_h exp(clamp(cs_t)) (dy_t h_in^T)
+//   dB_t = sum_{i >= kb} sum_l dS[l,t] C_l + sum_h w_t dt_t (x_t dst^T)
+//   dcs_off_t = pass(cs_t) exp(clamp(cs_t)) C_t . (dy_t h_in^T)        (per head)
+// (r2/dhammic-ai/src/kernels/ssd_scan.py:389-392 and :412-415 are the
+// forward terms whose adjoints these are; w_t = exp(clamp(cs_last - cs_t)).)
+//
+// The state terms are GEMMs over the group's heads, K = P per head. Their
+// per-token factors are applied to the per-head products (which the decay
+// gradient needs unscaled), results kept transposed ([n rows][token lanes]).
+// Each head's inputs (h_in, dst, the block's x and dy rows, cs, dt) are moved
+// into LDS by buffer_load ... lds, two heads ahead through a ring of three
+// slots, so no register holds staged data and the loads of two heads are in
+// flight while one computes. LDS rows are unpadded; 16-byte granules are
+// permuted per row so that transposed reads (h_in, dst) and row reads (x, dy)
+// hit distinct banks.
+#include "ssd_launch.h"
+#include "ssd_tile.h"
+
+namespace {
+
+// Permuted granule of logical granule g in row r of a W-wide bf16 tile.
+// Tiles read with ds_read_b64_tr_b16 (four rows, two granules per 16 lanes):
+template <int W>
+__device__ __forceinline__ int swz_tr(int r, int g) {
+  return W >= 64 ? g ^ ((r & 3) << 1) : g;
+}
+// Tiles read by rows (16 consecutive rows at one granule):
+template <int W>
+__device__ __forceinline__ int swz_nat(int r, int g) {
+  return W == 128 ? g ^ (r & 15) : (W == 64 ? g ^ ((r >> 1) & 7) : g ^ ((r >> 2) & 3));
+}
+
+// k-contiguous operand with i = mbase + L % 32 from a transposed-read tile
+// (row index k), as ttr_std does for padded tiles.
+template <int W>
+__device__ __forceinline__ bf16x4 swz_tr4(const bf16* t, int kb, int m0, int L) {
+  const int q = L & 15;
+  const int r = kb + (q >> 2), col = m0 + ((q & 3) << 2);
+  const bf16* p = t + r * W + (swz_tr<W>(r, col >> 3) << 3) + (col & 7);
+  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+template <int W>
+__device__ __forceinline__ bf16x8 swz_tr8(const bf16* t, int k0, int mbase, int L) {
+  const int h = L >> 5;
+  const int m0 = mbase + (((L >> 4) & 1) << 4);
+  return cat8(swz_tr4<W>(t, k0 + 8 * h, m0, L), swz_tr4<W>(t, k0 + 8 * h + 4, m0, L));
+}
+template <int W>
+__device__ __forceinline__ bf16x8 swz_nat8(const bf16* t, int r, int col) {
+  return *reinterpret_cast<const bf16x8*>(t + r * W + (swz_nat<W>(r, col >> 3) << 3));
+}
+
+template <int PT, int NT>
+struct GemmCfg {
+  static constexpr int PP = 32 * PT, NP = 32 * NT;
+  static constexpr int HIN = PP * NP;           // elements of h_in (and of dst)
+  static constexpr int XT = 64 * PP;            // elements of the x (and dy) rows
+  // bytes of one ring slot: h_in, dst, x, dy, then cs, dt, cs_last, spare (64 floats each)
+  static constexpr size_t kSlot = (size_t)(2 * HIN + 2 * XT) * 2 + 4 * 256;
+  static constexpr size_t bytes = 3 * kSlot;
+  // DMA instructions per wave and head (4 waves)
+  static constexpr int kTileDma = HIN / 512;    // 1 KB per instruction
+  static constexpr int kRowDma = XT / 512;
+  static constexpr int kPerWave = (2 * kTileDma + 2 * kRowDma) / 4 + 1;
+  static_assert((2 * kTileDma + 2 * kRowDma) % 4 == 0, "DMA split");
+};
+
+// vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt 7, lgkmcnt 15)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0xF70 | (N & 15) | ((N >> 4) << 14));
+}
+
+}  // namespace
+
+template <int PT, int NT>
+__global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __restrict__ chunks,
+                                                  const float* __restrict__ cs, const float* __restrict__ dt,
+                                                  const bf16* __restrict__ x, const bf16* __restrict__ dy,
+                                                  const bf16* __restrict__ hin, const bf16* __restrict__ dst,
+                                                  const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
+                                                  const float* __restrict__ dS, int nslices,
+                                                  float* __restrict__ dcs_off, bf16* __restrict__ dB,
+                                                  bf16* __restrict__ dC) {
+  using Cfg = GemmCfg<PT, NT>;
+  constexpr int PP = Cfg::PP, NP = Cfg::NP, NTW = (NT + 1) / 2, NK = PP / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int c = blockIdx.x, kb = blockIdx.y, g = blockIdx.z;
+  const ChunkInfo ci = chunks[c];
+  if (64 * kb >= ci.len) return;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int th = w & 1, nh = w >> 1;
+  int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
+  const int t_loc = 32 * th + l32;         // token of this lane within block kb
+  const int t = 64 * kb + t_loc;           // ... within the chunk
+  const bool tok = t < ci.len;
+  const int nrows = min(64, ci.len - 64 * kb);
+  const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
+  const int MC = d.max_chunks, Qpad = d.Qpad;
+  const int h0 = g * d.hpg, h1 = h0 + d.hpg;
+
+  // ---- one head's inputs into ring slot `slot` (kPerWave DMA instructions per wave) ----
+  auto issue = [&](int h, int slot) {
+    unsigned char* base = smem + slot * Cfg::kSlot;
+    const __amdgpu_buffer_rsrc_t rh = buf_rsrc(hin + ((int64_t)c * d.H + h) * Cfg::HIN);
+    const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dst + ((int64_t)c * d.H + h) * Cfg::HIN);
+    const int64_t xoff = (int64_t)(ci.row0 + 64 * kb) * xrow + (int64_t)h * d.P;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + xoff);
+    const __amdgpu_buffer_rsrc_t ry = buf_rsrc(dy + xoff);
+    // h_in and dst: rows p of NP elements, 512 / NP rows per instruction
+    constexpr int TG = NP / 8, TRI = 64 / TG;
+#pragma unroll
+    for (int q = 0; q < Cfg::kTileDma * 2 / 4; ++q) {
+      const int qq = w * (Cfg::kTileDma * 2 / 4) + q;  // 0 .. 2 kTileDma - 1
+      const bool second = qq >= Cfg::kTileDma;
+      const int qi = second ? qq - Cfg::kTileDma : qq;
+      const int r = qi * TRI + lane / TG, j = lane % TG;
+      const int off = (r * NP + (swz_tr<NP>(r, j) << 3)) * 2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          second ? rd : rh,
+          (__attribute__((address_space(3))) void*)(base + (second ? Cfg::HIN * 2 : 0) + qi * 1024), 16, off, 0, 0,
+          0);
+    }
+    // x and dy rows of the block: PP elements per row, 512 / PP rows per instruction
+    constexpr int XG = PP / 8, XRI = 64 / XG;
+#pragma unroll
+    for (int q = 0; q < Cfg::kRowDma * 2 / 4; ++q) {
+      const int qq = w * (Cfg::kRowDma * 2 / 4) + q;
+      const bool second = qq >= Cfg::kRowDma;
+      const int qi = second ? qq - Cfg::kRowDma : qq;
+      const int r = qi * XRI + lane / XG, j = lane % XG;
+      const int gcol = swz_nat<PP>(r, j) << 3;
+      const bool ok = r < nrows && gcol < d.P;
+      const int off = ok ? (int)((r * xrow + gcol) * 2) : SSD_BUF_SIZE;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          second ? ry : rx,
+          (__attribute__((address_space(3))) void*)(base + (2 * Cfg::HIN + (second ? Cfg::XT : 0)) * 2 + qi * 1024),
+          16, off, 0, 0, 0);
+    }
+    // cs of the block's tokens, dt, cs of the chunk's last position (4 bytes per lane)
+    unsigned char* sc = base + (2 * Cfg::HIN + 2 * Cfg::XT) * 2 + w * 256;
+    const float* csh = cs + ((int64_t)c * d.H + h) * Qpad;
+    int off;
+    __amdgpu_buffer_rsrc_t rs;
+    if (w == 1) {
+      rs = buf_rsrc(dt + (int64_t)(ci.row0 + 64 * kb) * d.H + h);
+      off = lane < nrows && d.has_dt ? lane * d.H * 4 : SSD_BUF_SIZE;
+    } else {
+      rs = buf_rsrc(csh);
+      off = w == 0 ? (64 * kb + lane) * 4 : (Qpad - 1) * 4;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)sc, 4, off, 0, 0, 0);
+  };
+
+  floatx16 aC[NTW], aB[NTW];
+#pragma unroll
+  for (int q = 0; q < NTW; ++q) {
+    zero(aC[q]);
+    zero(aB[q]);
+  }
+  // C[t][n] at this lane's accumulator rows n (the Y_off part of the decay gradient)
+  const __amdgpu_buffer_rsrc_t rC = buf_rsrc(Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
+  bf16x4 Cv[NTW][4];
+#pragma unroll
+  for (int q = 0; q < NTW; ++q) {
+    const int nt = nh * NTW + q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n0 = 32 * nt + 8 * r + 4 * hh;
+      const bool ok = tok && nt < NT && n0 < d.N;
+      Cv[q][r] = __builtin_bit_cast(
+          bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rC, ok ? (int)(t * brow + n0) * 2 : SSD_BUF_SIZE, 0, 0));
+    }
+  }
+
+  issue(h0, 0);
+  if (h0 + 1 < h1) issue(h0 + 1, 1);
+  for (int h = h0; h < h1; ++h) {
+    // this wave's loads of head h are done (those of h + 1 may still fly); then every wave's
+    if (h + 1 < h1) wait_vm<Cfg::kPerWave>();
+    else wait_vm<0>();
+    __syncthreads();  // head h visible in LDS; slot (h + 2) % 3 is free (head h - 1 done)
+    if (h + 2 < h1) issue(h + 2, (h + 2 - h0) % 3);
+    lane = opaque_lane();
+    hh = lane >> 5;
+    l32 = lane & 31;
+    const unsigned char* base = smem + ((h - h0) % 3) * Cfg::kSlot;
+    const bf16* th_ = reinterpret_cast<const bf16*>(base);
+    const bf16* td_ = th_ + Cfg::HIN;
+    const bf16* tx = td_ + Cfg::HIN;
+    const bf16* ty = tx + Cfg::XT;
+    const float* scal = reinterpret_cast<const float*>(ty + Cfg::XT);
+    const float cst = scal[t_loc], csl = scal[128];
+    const float dtt = d.has_dt ? scal[64 + t_loc] : 1.0f;
+    const float et = exp_clamp(cst), pt_ = clamp_pass(cst);
+    const float wdt = exp_clamp(csl - cst) * dtt;
+    bf16x8 yf[NK], xf[NK];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      yf[kk] = swz_nat8<PP>(ty, t_loc, 16 * kk + 8 * hh);
+      xf[kk] = swz_nat8<PP>(tx, t_loc, 16 * kk + 8 * hh);
+    }
+    float osum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NTW; ++q) {
+      const int nt = nh * NTW + q;
+      if (nt >= NT) continue;
+      floatx16 T, U;
+      zero(T);
+      zero(U);
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        mfma(T, swz_tr8<NP>(th_, 16 * kk, 32 * nt, lane), yf[kk]);
+        mfma(U, swz_tr8<NP>(td_, 16 * kk, 32 * nt, lane), xf[kk]);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        aC[q][v] = fmaf(et, T[v], aC[q][v]);
+        aB[q][v] = fmaf(wdt, U[v], aB[q][v]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) osum += (float)Cv[q][r][e] * T[4 * r + e];
+    }
+    osum += __shfl_xor(osum, 32, 64);
+    if (hh == 0 && tok) dcs_off[((int64_t)nh * MC * d.H + (int64_t)c * d.H + h) * Qpad + t] = osum * et * pt_;
+  }
+
+  // ---- tile terms: dC += dS[kb, j] B_j (j <= kb), dB += dS[i, kb]^T C_i (i >= kb) ----
+  constexpr int PI = tpitch_tr<NP>();
+  bf16* tBC = reinterpret_cast<bf16*>(smem);         // [64][NP], padded
+  bf16* tS = tBC + tsize<64, NP, PI>();              // [64][64] bf16, padded
+  const int nb = Qpad / 64;
+  const int nbl = (ci.len + 63) >> 6;
+  const int64_t sstride = (int64_t)MC * d.G * nb * nb * 4096;
+  const float* dSc = dS + ((int64_t)c * d.G + g) * nb * nb * 4096;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int lo = pass == 0 ? 0 : kb, hi = pass == 0 ? kb : nbl - 1;
+    for (int m = lo; m <= hi; ++m) {
+      __syncthreads();
+      const int ti = pass == 0 ? kb : m, tj = pass == 0 ? m : kb;
+      const float* src = dSc + (ti * nb + tj) * 4096;
+      for (int id = threadIdx.x; id < 512; id += 256) {
+        const int r = id >> 3, k = (id & 7) * 8;
+        floatx4 s0 = *reinterpret_cast<const floatx4*>(src + r * 64 + k);
+        floatx4 s1 = *reinterpret_cast<const floatx4*>(src + r * 64 + k + 4);
+        for (int sl = 1; sl < nslices; ++sl) {
+          s0 += *reinterpret_cast<const floatx4*>(src + sl * sstride + r * 64 + k);
+          s1 += *reinterpret_cast<const floatx4*>(src + sl * sstride + r * 64 + k + 4);
+        }
+        bf16x8 v;
+        v[0] = (bf16)s0[0]; v[1] = (bf16)s0[1]; v[2] = (bf16)s0[2]; v[3] = (bf16)s0[3];
+        v[4] = (bf16)s1[0]; v[5] = (bf16)s1[1]; v[6] = (bf16)s1[2]; v[7] = (bf16)s1[3];
+        *reinterpret_cast<bf16x8*>(tS + toff<64, tpitch<64>()>(r, k)) = v;
+      }
+      {
+        TileStage<64, NP, 256> st;
+        tstage_load_v(st, (pass == 0 ? Bm : Cm) + (int64_t)(ci.row0 + 64 * m) * brow + (int64_t)g * d.N, brow,
+                      min(64, ci.len - 64 * m), d.N);
+        tstage_store<64, NP, 256, PI>(st, tBC);
+      }
+      __syncthreads();
+      lane = opaque_lane();
+      hh = lane >> 5;
+#pragma unroll
+      for (int q = 0; q < NTW; ++q) {
+        const int nt = nh * NTW + q;
+        if (nt >= NT) continue;
+#pragma unroll
+        for (int kk = 0; kk < 64; kk += 16) {
+          const bf16x8 av = ttr_std<NP, PI>(tBC, kk, 32 * nt, lane);
+          // pass 0: B[k = s][j = t] = dS[t][s] (row t, natural); pass 1: B[k = l][j = t] (transposed)
+          if (pass == 0)
+            mfma(aC[q], av, tld8<64, tpitch<64>()>(tS, t_loc, kk + 8 * hh));
+          else
+            mfma(aB[q], av, ttr_std<64, tpitch<64>()>(tS, kk, 32 * th, lane));
+        }
+      }
+    }
+  }
+  if (tok) {
+    const int64_t row = (int64_t)(ci.row0 + t) * brow + (int64_t)g * d.N;
+#pragma unroll
+    for (int q = 0; q < NTW; ++q) {
+      const int nt = nh * NTW + q;
+      if (nt >= NT) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n0 = 32 * nt + 8 * r + 4 * hh;
+        if (n0 >= d.N) continue;
+        bf16x4 oc, ob;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          oc[e] = (bf16)aC[q][4 * r + e];
+          ob[e] = (bf16)aB[q][4 * r + e];
+        }
+        *reinterpret_cast<bf16x4*>(dC + row + n0) = oc;
+        *reinterpret_cast<bf16x4*>(dB + row + n0) = ob;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+size_t lds_bwd_gemm(const SsdDims& d) {
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return GemmCfg<1, 1>::bytes;
+    case 12: return GemmCfg<1, 2>::bytes;
+    case 14: return GemmCfg<1, 4>::bytes;
+    case 21: return GemmCfg<2, 1>::bytes;
+    case 22: return GemmCfg<2, 2>::bytes;
+    default: return GemmCfg<2, 4>::bytes;
+  }
+}
+
+template <int PT, int NT>
+static hipError_t bwd_gemm_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dB, void* dC,
+                             hipStream_t s) {
+  ensure_lds(k_bwd_gemm<PT, NT>, GemmCfg<PT, NT>::bytes);
+  hipLaunchKernelGGL((k_bwd_gemm<PT, NT>), dim3(d.max_chunks, d.Qpad / 64, d.G), dim3(256), (GemmCfg<PT, NT>::bytes), s,
+                     d, b.chunks, b.cs, in.dt, reinterpret_cast<const bf16*>(in.x),
+                     reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(b.hin), b.dst16,
+                     reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), b.dS_tiles,
+                     b.nslices, b.dcs_off, reinterpret_cast<bf16*>(dB), reinterpret_cast<bf16*>(dC));
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_gemm(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dB, void* dC,
+                           hipStream_t s) {
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return bwd_gemm_t<1, 1>(d, b, in, dy, dB, dC, s);
+    case 12: return bwd_gemm_t<1, 2>(d, b, in, dy, dB, dC, s);
+    case 14: return bwd_gemm_t<1, 4>(d, b, in, dy, dB, dC, s);
+    case 21: return bwd_gemm_t<2, 1>(d, b, in, dy, dB, dC, s);
+    case 22: return bwd_gemm_t<2, 2>(d, b, in, dy, dB, dC, s);
+    default: return bwd_gemm_t<2, 4>(d, b, in, dy, dB, dC, s);
+  }
+}

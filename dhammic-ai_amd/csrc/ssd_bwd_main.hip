@@ -10,15 +10,14 @@
 //   dX_s   = sum_l M[l,s] dy_l + w_s B_s dst^T           (dx = dt dX + D dy)
 //   rowG_l = sum_s G[l,s],  colG_s = sum_l G[l,s]
 //   E_s    = pass_w(s) dt_s x_s . (w_s B_s dst^T),  xdx_s = x_s . dX_s
-//   dcs_off_l = pass(cs_l) C_l . (exp(cs_l) dy_l h_in)
 // and, summed over the heads of the group,
-//   dS[l,s] = sum_h dm L                   (-> dB = dS^T C, dC = dS B, kernel k_bwd_bc)
-//   dBs_s   = sum_h w_s dt_s x_s dst       (state part of dB)
-//   dCo_l   = sum_h exp(cs_l) dy_l h_in    (Y_off part of dC)
+//   dS[l,s] = sum_h dm L                   (-> dB = dS^T C, dC = dS B, kernel k_bwd_gemm)
+// The head-summed state terms of dB and dC and the Y_off part of the decay
+// gradient are k_bwd_gemm's (ssd_bwd_gemm.hip).
 //
 // k_bwd_main: one block per (column block j, chunk, group, head slice). The
-// block owns the 64 columns s of block j, so dX, colG and the state part of dB
-// are complete there; it walks the tiles (i, j), i >= j, of every head of its
+// block owns the 64 columns s of block j, so dX and colG are complete there;
+// it walks the tiles (i, j), i >= j, of every head of its
 // slice. S for those tiles is computed once per block and kept in registers;
 // dS accumulates in registers over the slice's heads. Tiles are computed
 // transposed ([s rows][l lanes]): row sums of G are per-lane, column sums are
@@ -32,7 +31,6 @@
 struct BwdMainArgs {
   const ChunkInfo* chunks;
   const float* cs;    // [MC][H][Qpad]
-  const bf16* hin;    // [MC][H][Ppad][Npad]
   const bf16* dst;    // [MC][H][Ppad][Npad], gradient leaving each chunk (bf16)
   const bf16* x;
   const float* dt;
@@ -45,11 +43,8 @@ struct BwdMainArgs {
   float* colG;        // [MC][H][Qpad]
   float* eterm;
   float* xdx;
-  float* dcs_off;
   float* dD_part;     // [MC][H][Qpad/64]
   float* dS;          // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
-  float* dBs;         // [nslices][R][G][N]
-  float* dCo;         // [nslices][R][G][N]
   int nslices, hslice;
 };
 
@@ -62,7 +57,7 @@ struct BwdMainLds {
   static size_t bytes(int Qpad) {
     const size_t xch = 2 * PT * 4096;
     return sizeof(float) * (2 * Qpad + RED) +
-           2 * (size_t)(5 * tsize<64, PP>() + 2 * tsize<PP, NP>() + tsize<64, NP>() + 4 * tsize<32, 32>()) + xch;
+           2 * (size_t)(5 * tsize<64, PP>() + tsize<PP, NP>() + tsize<64, NP>() + 4 * tsize<32, 32>()) + xch;
   }
 };
 
@@ -111,8 +106,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   bf16* xj = reinterpret_cast<bf16*>(red + BwdMainLds<PT, NT>::RED);  // [64][PP]
   bf16* dYt = xj + XT;                             // [4][64][PP] (blocks j .. nbl-1 used)
   bf16* dstT = dYt + 4 * XT;                       // [PP][NP]
-  bf16* hinT = dstT + ST;                          // [PP][NP]
-  bf16* Bt = hinT + ST;                            // [64][NP]
+  bf16* Bt = dstT + ST;                            // [64][NP]
   bf16* Mb = Bt + BTS + w * MT;                    // this wave's [32][32]
   float* xch = reinterpret_cast<float*>(Bt + BTS + 4 * MT);
 
@@ -154,16 +148,10 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     S[t][1] = acc_frag(sacc, 1);
   }
 
-  // per-token lane of the state terms: token 32 wr + l32 of block j, n tiles nt = 2 ntk + wc
+  // per-token lane of the state terms: token 32 wr + l32 of block j
   const int t_loc = 32 * wr + l32;
   const int tg = 64 * j + t_loc;
   const bool t_ok = tg < ci.len;
-  floatx16 dBT[NTW], dCoT[NTW];
-#pragma unroll
-  for (int ntk = 0; ntk < NTW; ++ntk) {
-    zero(dBT[ntk]);
-    zero(dCoT[ntk]);
-  }
 
   // Inputs of the tile phase (x, dy, cs, dt) are loaded during the previous
   // head's state phase; those of the state phase (dst, h_in) during this
@@ -191,6 +179,11 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   load_tiles(h_lo);
   for (int h = h_lo; h < h_hi; ++h) {
     lane = opaque_lane();
+#pragma unroll
+    for (int t = 0; t < kMaxSlots; ++t) {
+      launder(S[t][0]);
+      launder(S[t][1]);
+    }
     hh = lane >> 5;
     l32 = lane & 31;
     __syncthreads();  // the previous head's LDS reads are done
@@ -204,9 +197,8 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     for (int t = 0; t < kMaxSlots; ++t)
       if (t < nt_i) tstage_store(hs.y[t], dYt + (j + t) * XT);
     __syncthreads();
-    TileStage<PP, NP, 256> sd, sh;
+    TileStage<PP, NP, 256> sd;
     tstage_load_v(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
-    tstage_load_v(sh, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
 
     const float cs_last = s_cs2[Qpad - 1];
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
@@ -304,7 +296,6 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       if (sg < ci.len) a.colG[((int64_t)c * d.H + h) * Qpad + sg] = red_col[threadIdx.x] + red_col[64 + threadIdx.x];
     }
     tstage_store(sd, dstT);
-    tstage_store(sh, hinT);
     __syncthreads();
     if (h + 1 < h_hi) load_tiles(h + 1);
 
@@ -350,59 +341,10 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     esum += __shfl_xor(esum, 32, 64);
     xsum += __shfl_xor(xsum, 32, 64);
 
-    // dB state part: dBs^T[n][s] += sum_p dst[p][n] (w_s dt_s x[s][p])
-    // dC Y_off part: dCo^T[n][l] += sum_p h_in[p][n] (e^{cs_l} dy[l][p]); dcs_off
-    // The per-token factors are folded into the token-side operand, so both
-    // accumulators are updated by MFMA only; dcs_off needs the unscaled
-    // product h_in dy^T per head (tc).
-    const float el = t_ok ? exp2_fast(clamp_med3(cs_t, -SSD_T2, SSD_T2)) : 0.0f;
-    const float pl = fabsf(cs_t) < SSD_T2 ? 1.0f : 0.0f;
-    const float wsd = ws * dts;
-    float osum = 0.0f;
-    const bf16* crow = a.Cm + (int64_t)(ci.row0 + (t_ok ? tg : 0)) * brow + (int64_t)g * d.N;
-    bf16x8 xs[PP / 16], ys[PP / 16], yr[PP / 16];
-#pragma unroll
-    for (int kq = 0; kq < PP / 16; ++kq) {
-      const bf16x8 xb = tld8<PP>(xj, t_loc, 16 * kq + 8 * hh);
-      yr[kq] = tld8<PP>(dyc, t_loc, 16 * kq + 8 * hh);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xs[kq][e] = (bf16)((float)xb[e] * wsd);
-        ys[kq][e] = (bf16)((float)yr[kq][e] * el);
-      }
-    }
-#pragma unroll
-    for (int ntk = 0; ntk < NTW; ++ntk) {
-      const int nt = 2 * ntk + wc;
-      if (nt >= NT) continue;
-      floatx16 tc;
-      zero(tc);
-#pragma unroll
-      for (int kq = 0; kq < PP / 16; ++kq) {
-        const bf16x8 dA = ttr_std<NP>(dstT, 16 * kq, 32 * nt, lane);
-        const bf16x8 hA = ttr_std<NP>(hinT, 16 * kq, 32 * nt, lane);
-        mfma(dBT[ntk], dA, xs[kq]);
-        mfma(dCoT[ntk], hA, ys[kq]);
-        mfma(tc, hA, yr[kq]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n0 = 32 * nt + 8 * r + 4 * hh;
-        bf16x4 cq;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cq[e] = (bf16)0.0f;
-        if (t_ok && n0 < d.N) cq = *reinterpret_cast<const bf16x4*>(crow + n0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) osum += tc[4 * r + e] * (float)cq[e];
-      }
-    }
-    osum *= el;
-    osum += __shfl_xor(osum, 32, 64);
     for (int o = 32; o > 0; o >>= 1) dpart += __shfl_xor(dpart, o, 64);
     if (hh == 0) {
       red_e[wc * 64 + t_loc] = esum * dts * pw;
       red_x[wc * 64 + t_loc] = xsum;
-      red_o[wc * 64 + t_loc] = osum * pl;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -411,7 +353,6 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
         const int64_t o = ((int64_t)c * d.H + h) * Qpad + tgg;
         a.eterm[o] = red_e[tl] + red_e[64 + tl];
         a.xdx[o] = red_x[tl] + red_x[64 + tl];
-        a.dcs_off[o] = red_o[tl] + red_o[64 + tl];
       }
     }
     for (int e = threadIdx.x; e < nt_i * 64; e += 256) {
@@ -428,7 +369,6 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   }
 
   // ---- outputs summed over the slice's heads ----
-  const int64_t sl_off = (int64_t)slc * d.R * brow;
   float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
 #pragma unroll
   for (int t = 0; t < kMaxSlots; ++t) {
@@ -443,127 +383,6 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
       q[2] = dS[t][4 * r + 2];
       q[3] = dS[t][4 * r + 3];
       *reinterpret_cast<floatx4*>(tile + l_loc * 64 + 32 * wr + 8 * r + 4 * hh) = q;
-    }
-  }
-  if (t_ok) {
-    float* ob = a.dBs + sl_off + (int64_t)(ci.row0 + tg) * brow + (int64_t)g * d.N;
-    float* oc = a.dCo + sl_off + (int64_t)(ci.row0 + tg) * brow + (int64_t)g * d.N;
-#pragma unroll
-    for (int ntk = 0; ntk < NTW; ++ntk) {
-      const int nt = 2 * ntk + wc;
-      if (nt >= NT) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n0 = 32 * nt + 8 * r + 4 * hh;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n0 + e < d.N) {
-            ob[n0 + e] = dBT[ntk][4 * r + e];
-            oc[n0 + e] = dCoT[ntk][4 * r + e];
-          }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dB and dC of block k of a chunk (one block per (chunk, block, group)):
-//   dC_l = dCo_l + sum_{j <= k} sum_s dS[k,j][l,s] B_s
-//   dB_s = dBs_s + sum_{i >= k} sum_l dS[i,k][l,s] C_l
-// summed over the head slices, computed transposed ([n][token]) on MFMA.
-// ---------------------------------------------------------------------------
-template <int NT>
-__global__ void __launch_bounds__(256) k_bwd_bc(SsdDims d, BwdMainArgs a, bf16* __restrict__ dB,
-                                                bf16* __restrict__ dC) {
-  constexpr int NP = 32 * NT, NTW = (NT + 1) / 2;
-  __shared__ __align__(16) bf16 tBC[tsize<64, NP>()];
-  __shared__ __align__(16) bf16 tS[tsize<64, 64>()];
-  const int nb = d.Qpad / 64;
-  const int c = blockIdx.x, kb = blockIdx.y, g = blockIdx.z;
-  const ChunkInfo ci = a.chunks[c];
-  const int nbl = (ci.len + 63) >> 6;
-  if (kb >= nbl) return;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w & 1, wc = w >> 1;
-  const int hh = lane >> 5, l32 = lane & 31;
-  const int64_t brow = (int64_t)d.G * d.N;
-  const int64_t tstride = (int64_t)d.max_chunks * d.G * nb * nb * 4096;  // per slice
-  const float* dSc = a.dS + ((int64_t)c * d.G + g) * (int64_t)(nb * nb) * 4096;
-
-  auto stage_dS = [&](int i, int j) {
-    const float* src = dSc + (int64_t)(i * nb + j) * 4096;
-    for (int id = threadIdx.x; id < 512; id += 256) {  // 8 floats per id
-      const int r = id >> 3, k = (id & 7) * 8;
-      floatx4 s0 = *reinterpret_cast<const floatx4*>(src + r * 64 + k);
-      floatx4 s1 = *reinterpret_cast<const floatx4*>(src + r * 64 + k + 4);
-      for (int sl = 1; sl < a.nslices; ++sl) {
-        const float* p = src + sl * tstride + r * 64 + k;
-        s0 += *reinterpret_cast<const floatx4*>(p);
-        s1 += *reinterpret_cast<const floatx4*>(p + 4);
-      }
-      bf16x8 v;
-      v[0] = (bf16)s0[0]; v[1] = (bf16)s0[1]; v[2] = (bf16)s0[2]; v[3] = (bf16)s0[3];
-      v[4] = (bf16)s1[0]; v[5] = (bf16)s1[1]; v[6] = (bf16)s1[2]; v[7] = (bf16)s1[3];
-      *reinterpret_cast<bf16x8*>(tS + toff<64>(r, k)) = v;
-    }
-  };
-  auto stage_bc = [&](const bf16* src, int blk) {
-    TileStage<64, NP, 256> st;
-    tstage_load_v(st, src + (int64_t)(ci.row0 + 64 * blk) * brow + (int64_t)g * d.N, brow,
-                min(64, ci.len - 64 * blk), d.N);
-    tstage_store(st, tBC);
-  };
-
-  // wave (wr, wc): tokens 32 wr + l32 of block kb, n tiles nt = 2 ntk + wc
-  floatx16 acc[NTW];
-  for (int pass = 0; pass < 2; ++pass) {
-    // pass 0: dC (tiles (kb, j), j <= kb, with B_j); pass 1: dB (tiles (i, kb), i >= kb, with C_i)
-#pragma unroll
-    for (int q = 0; q < NTW; ++q) zero(acc[q]);
-    const int lo = pass == 0 ? 0 : kb, hi = pass == 0 ? kb : nbl - 1;
-    for (int m = lo; m <= hi; ++m) {
-      __syncthreads();
-      if (pass == 0) {
-        stage_dS(kb, m);
-        stage_bc(a.Bm, m);
-      } else {
-        stage_dS(m, kb);
-        stage_bc(a.Cm, m);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < NTW; ++q) {
-        const int nt = 2 * q + wc;
-        if (nt >= NT) continue;
-#pragma unroll
-        for (int kk = 0; kk < 64; kk += 16) {
-          const bf16x8 av = ttr_std<NP>(tBC, kk, 32 * nt, lane);
-          // pass 0: B[k = s][j = l] = dS[l][s] (row l, natural); pass 1: B[k = l][j = s] (transposed)
-          const bf16x8 bv = pass == 0 ? tld8<64>(tS, 32 * wr + l32, kk + 8 * hh) : ttr_std<64>(tS, kk, 32 * wr, lane);
-          mfma(acc[q], av, bv);
-        }
-      }
-    }
-    const int tok = 64 * kb + 32 * wr + l32;
-    if (tok < ci.len) {
-      const float* extra = pass == 0 ? a.dCo : a.dBs;
-      bf16* out = pass == 0 ? dC : dB;
-      const int64_t row = (int64_t)(ci.row0 + tok) * brow + (int64_t)g * d.N;
-#pragma unroll
-      for (int q = 0; q < NTW; ++q) {
-        const int nt = 2 * q + wc;
-        if (nt >= NT) continue;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int n0 = 32 * nt + 8 * r + 4 * hh;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n0 + e >= d.N) continue;
-            float v = acc[q][4 * r + e];
-            for (int sl = 0; sl < a.nslices; ++sl) v += extra[(int64_t)sl * d.R * brow + row + n0 + e];
-            out[row + n0 + e] = (bf16)v;
-          }
-        }
-      }
     }
   }
 }
@@ -598,19 +417,10 @@ static hipError_t bwd_main_t(const SsdDims& d, const BwdMainArgs& a, hipStream_t
   return hipGetLastError();
 }
 
-template <int NT>
-static hipError_t bwd_bc_t(const SsdDims& d, const BwdMainArgs& a, void* dB, void* dC, hipStream_t s) {
-  dim3 grid(d.max_chunks, d.Qpad / 64, d.G);
-  hipLaunchKernelGGL((k_bwd_bc<NT>), grid, dim3(256), 0, s, d, a, reinterpret_cast<bf16*>(dB),
-                     reinterpret_cast<bf16*>(dC));
-  return hipGetLastError();
-}
-
 static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx) {
   BwdMainArgs a;
   a.chunks = b.chunks;
   a.cs = b.cs;
-  a.hin = reinterpret_cast<const bf16*>(b.hin);
   a.dst = b.dst16;
   a.x = reinterpret_cast<const bf16*>(in.x);
   a.dt = in.dt;
@@ -623,11 +433,8 @@ static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdI
   a.colG = b.colG;
   a.eterm = b.eterm;
   a.xdx = b.xdx;
-  a.dcs_off = b.dcs_off;
   a.dD_part = b.dD_part;
   a.dS = b.dS_tiles;
-  a.dBs = b.dB_part;
-  a.dCo = b.dC_part;
   a.nslices = b.nslices;
   a.hslice = b.hslice;
   return a;
@@ -643,15 +450,6 @@ hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, 
     case 21: return bwd_main_t<2, 1>(d, a, s);
     case 22: return bwd_main_t<2, 2>(d, a, s);
     default: return bwd_main_t<2, 4>(d, a, s);
-  }
-}
-
-hipError_t launch_bwd_bc(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* dB, void* dC, hipStream_t s) {
-  const BwdMainArgs a = make_main_args(d, b, in, nullptr, nullptr);
-  switch (d.Npad / 32) {
-    case 1: return bwd_bc_t<1>(d, a, dB, dC, s);
-    case 2: return bwd_bc_t<2>(d, a, dB, dC, s);
-    default: return bwd_bc_t<4>(d, a, dB, dC, s);
   }
 }
 

@@ -3,7 +3,7 @@
 
 #include <initializer_list>
 
-#include "../../include/ssd_mi355x.h"
+#include "ssd_mi355x.h"
 #include "ssd_launch.h"
 
 namespace {
@@ -69,7 +69,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->state_dtype = s->state_dtype;
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
   if ((scan_fwd_chunk_supported(p->dtype, d) ? lds_scan_fwd_chunk(d) : lds_chunk_scan_fwd(p->dtype, d)) > kMaxLds ||
-      (p->fused_bwd ? lds_bwd_main(d) > kMaxLds
+      (p->fused_bwd ? (lds_bwd_main(d) > kMaxLds || lds_bwd_gemm(d) > kMaxLds)
                     : (lds_bwd_col(p->dtype, d) > kMaxLds || lds_bwd_row(p->dtype, d) > kMaxLds)))
     return SSD_ERR_UNSUPPORTED;
 
@@ -113,17 +113,18 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_rowG = take((size_t)p->nrowg * MC * H * d.Qpad * sizeof(float));
   p->o_colG = take(MC * H * d.Qpad * sizeof(float));
   p->o_eterm = take(MC * H * d.Qpad * sizeof(float));
-  p->o_dcs = take(MC * H * d.Qpad * sizeof(float));
+  p->o_dcs = take((p->fused_bwd ? 2 : 1) * MC * H * d.Qpad * sizeof(float));
   p->o_xdx = take(MC * H * d.Qpad * sizeof(float));
   p->o_dD = take(MC * H * (d.Qpad / SSD_BLK) * sizeof(float));
   p->o_dA = take(MC * H * sizeof(float));
   const size_t bcn = (size_t)R * d.G * d.N * sizeof(float);
-  const bool parts = p->fused_bwd || p->nslices > 1;
+  const bool parts = p->nslices > 1;
   p->o_dBp = parts ? take(p->nslices * bcn) : 0;
   p->o_dCp = parts ? take(p->nslices * bcn) : 0;
   const size_t nbq = (size_t)(d.Qpad / SSD_BLK);
-  p->o_dS = p->fused_bwd ? take((size_t)p->nslices * MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
-  p->o_dst16 = p->fused_bwd ? take(MC * H * PN * 2) : 0;
+  const bool tiles = p->fused_bwd;
+  p->o_dS = tiles ? take((size_t)p->nslices * MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
+  p->o_dst16 = tiles ? take(MC * H * PN * 2) : 0;
   p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
   p->bwd_bytes = off;
   return SSD_OK;
@@ -143,6 +144,7 @@ void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
   b->norm_blocks = (int)p.norm_blocks;
   b->fused_bwd = p.fused_bwd;
   b->nrowg = p.nrowg;
+  b->ndcs = p.fused_bwd ? 2 : 1;
 }
 
 void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
@@ -157,11 +159,12 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->xdx = reinterpret_cast<float*>(s + p.o_xdx);
   b->dD_part = reinterpret_cast<float*>(s + p.o_dD);
   b->dA_part = reinterpret_cast<float*>(s + p.o_dA);
-  const bool parts = p.fused_bwd || p.nslices > 1;
+  const bool parts = p.nslices > 1;
   b->dB_part = parts ? reinterpret_cast<float*>(s + p.o_dBp) : nullptr;
   b->dC_part = parts ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
-  b->dS_tiles = p.fused_bwd ? reinterpret_cast<float*>(s + p.o_dS) : nullptr;
-  b->dst16 = p.fused_bwd ? reinterpret_cast<bf16*>(s + p.o_dst16) : nullptr;
+  const bool tiles = p.fused_bwd;
+  b->dS_tiles = tiles ? reinterpret_cast<float*>(s + p.o_dS) : nullptr;
+  b->dst16 = tiles ? reinterpret_cast<bf16*>(s + p.o_dst16) : nullptr;
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
 }
 
@@ -287,6 +290,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   // the fused backward needs 16-byte vector access; otherwise the column / row kernels run
   const bool fused = p.fused_bwd && d.vec_x && d.vec_bc;
   if (!fused) {
+    b.ndcs = 1;
     b.nrowg = 1;           // column / row kernels write one rowG partial
     b.dst16 = nullptr;     // and read dst in fp32
   }
@@ -311,7 +315,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   if (fused) {
     // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
     SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_main(d, b, in, dY, a->dx, s));
-    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_bc(d, b, in, a->dB, a->dC, s));
+    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_gemm(d, b, in, dY, a->dB, a->dC, s));
   } else {
     SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));
     SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, d, b, in, dY, a->dC, s));

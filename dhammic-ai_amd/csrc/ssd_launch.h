@@ -75,7 +75,11 @@ size_t lds_bwd_main(const SsdDims& d);
 int bwd_main_num_sets(const SsdDims& d);
 hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
                            hipStream_t s);
-hipError_t launch_bwd_bc(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* dB, void* dC, hipStream_t s);
+
+// ssd_bwd_gemm.hip (fused path): dB, dC and the Y_off part of the decay gradient
+size_t lds_bwd_gemm(const SsdDims& d);
+hipError_t launch_bwd_gemm(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dB, void* dC,
+                           hipStream_t s);
 
 // ssd_norm.hip
 hipError_t launch_gated_norm_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,

@@ -36,16 +36,17 @@ struct SsdBufs {
   float* rowG;             // [nrowg][max_chunks][H][Qpad] (partials summed by the finish kernel)
   float* colG;             // [max_chunks][H][Qpad]
   float* eterm;            // [max_chunks][H][Qpad]
-  float* dcs_off;          // [max_chunks][H][Qpad]
+  float* dcs_off;          // [ndcs][max_chunks][H][Qpad] (partials summed by the finish kernel)
   float* xdx;              // [max_chunks][H][Qpad]
   float* dD_part;          // [max_chunks][H][Qpad/64]
   float* dA_part;          // [max_chunks][H]
-  float* dB_part;          // [nslices][R][G][N] (fused path: state part of dB)
-  float* dC_part;          // [nslices][R][G][N] (fused path: Y_off part of dC)
+  float* dB_part;          // [nslices][R][G][N] (column / row kernels)
+  float* dC_part;          // [nslices][R][G][N]
   float* dS_tiles;         // fused path: [nslices][max_chunks][G][nb*nb][64][64] head-summed dS
   float* dw_part;          // [norm_blocks][H*P]
   int npass_blk, nslices, hslice, norm_blocks;
-  int fused_bwd;           // 1: k_bwd_main + k_bwd_bc (bf16), 0: column / row kernels
+  int fused_bwd;           // 1: k_bwd_main + k_bwd_gemm (bf16), 0: column / row kernels
+  int ndcs;                // dcs_off partials
   int nrowg;               // rowG partials (column sets of the fused path, else 1)
 };
 

@@ -141,6 +141,11 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
   load_head(h_lo);
   for (int h = h_lo; h < h_hi; ++h) {
     lane = opaque_lane();
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      launder(S[u][0]);
+      launder(S[u][1]);
+    }
     __syncthreads();  // the previous head's LDS reads are done
 #pragma unroll
     for (int i = 0; i < NB; ++i)

@@ -79,6 +79,11 @@ __device__ __forceinline__ bf16x4 ttr4(const bf16* t, int kb, int m0, int L) {
   return __builtin_bit_cast(bf16x4, v);
 }
 
+// Makes v opaque to the optimizer at this point. Used at the top of long loops
+// on loop-invariant bf16 register tiles: otherwise their bf16 -> fp32
+// conversions are hoisted out of the loop and the tile takes twice the registers.
+__device__ __forceinline__ void launder(bf16x8& v) { asm volatile("" : "+v"(v)); }
+
 __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
