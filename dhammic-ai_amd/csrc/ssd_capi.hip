@@ -1,6 +1,7 @@
 // extern "C" entry points: validation, workspace layout, launch sequences.
 #include <string.h>
 
+#include <algorithm>
 #include <initializer_list>
 
 #include "ssd_mi355x.h"
@@ -21,7 +22,7 @@ struct Plan {
   int dtype, state_dtype;
   int64_t nslices, hslice, npass_blk, norm_blocks;
   // byte offsets inside each workspace
-  size_t o_chunks, o_seq0, o_cs, o_hin, o_ypre, o_rstd, saved_bytes;
+  size_t o_chunks, o_seq0, o_cs, o_fast, o_hin, o_ypre, o_rstd, saved_bytes;
   size_t o_st, fwd_bytes;
   size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dst16, bwd_bytes;
   int fused_bwd, nrowg;
@@ -68,7 +69,8 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->dtype = s->dtype;
   p->state_dtype = s->state_dtype;
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
-  if ((scan_fwd_chunk_supported(p->dtype, d) ? lds_scan_fwd_chunk(d) : lds_chunk_scan_fwd(p->dtype, d)) > kMaxLds ||
+  if ((scan_fwd_chunk_supported(p->dtype, d) ? std::max(lds_scan_fwd_chunk(d), lds_scan_fwd_fact(d))
+                                              : lds_chunk_scan_fwd(p->dtype, d)) > kMaxLds ||
       (p->fused_bwd ? (lds_bwd_main(d) > kMaxLds || lds_bwd_gemm(d) > kMaxLds)
                     : (lds_bwd_col(p->dtype, d) > kMaxLds || lds_bwd_row(p->dtype, d) > kMaxLds)))
     return SSD_ERR_UNSUPPORTED;
@@ -99,6 +101,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_chunks = take(MC * sizeof(ChunkInfo));
   p->o_seq0 = take((nseq + 1) * sizeof(int32_t));
   p->o_cs = take(MC * H * d.Qpad * sizeof(float));
+  p->o_fast = take(MC * H * sizeof(int32_t));
   p->o_hin = take(MC * H * PN * es);
   p->o_ypre = d.has_z ? take((size_t)R * H * d.P * es) : 0;
   p->o_rstd = d.has_z ? take((size_t)R * sizeof(float)) : 0;
@@ -135,6 +138,7 @@ void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
   b->chunks = reinterpret_cast<ChunkInfo*>(s + p.o_chunks);
   b->seq_chunk0 = reinterpret_cast<int32_t*>(s + p.o_seq0);
   b->cs = reinterpret_cast<float*>(s + p.o_cs);
+  b->fast = reinterpret_cast<int32_t*>(s + p.o_fast);
   b->hin = s + p.o_hin;
   b->ypre = p.d.has_z ? s + p.o_ypre : nullptr;
   b->rstd = p.d.has_z ? reinterpret_cast<float*>(s + p.o_rstd) : nullptr;
@@ -260,9 +264,13 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
                                     desc->want_final ? a->final_state : nullptr, s));
   }
   void* yout = d.has_z ? b.ypre : a->y;
-  if (scan_fwd_chunk_supported(p.dtype, d) && d.vec_x && d.vec_bc)
-    SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_scan_fwd_chunk(d, b, in, yout, s));
-  else
+  if (scan_fwd_chunk_supported(p.dtype, d) && d.vec_x && d.vec_bc) {
+    // factorised decay, then the exact kernel on the (chunk, head) pairs it cannot take
+    SSD_TRY(tm.begin(SSD_PH_FWD_SCAN));
+    SSD_TRY(launch_scan_fwd_fact(d, b, in, yout, s));
+    SSD_TRY(launch_scan_fwd_chunk(d, b, in, yout, b.fast, s));
+    SSD_TRY(tm.end(SSD_PH_FWD_SCAN));
+  } else
     SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, yout, s));
   if (d.has_z) SSD_PHASE(tm, SSD_PH_NORM_FWD, launch_gated_norm_fwd(p.dtype, d, b, in, a->y, s));
   return SSD_OK;

@@ -26,6 +26,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define SSD_BLK 64
 #define SSD_LO (-20.0f)
 #define SSD_HI (20.0f)
+// Largest drop of the in-chunk cumsum over one 64-token block (nats) for which
+// the factorised decay exp(cs_l - cs_s) = exp(cs_l - c) * exp(c - cs_s) is used.
+#define SSD_FACT_RANGE (64.0f)
 
 // exp(clamp(v, -20, 20)): every decay exponent of the reference path
 // (r2/dhammic-ai/src/kernels/ssd_scan.py:53-54, :116, :212).

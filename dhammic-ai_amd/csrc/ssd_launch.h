@@ -52,7 +52,15 @@ hipError_t launch_state_bwd_fused(const SsdDims& d, const SsdBufs& b, const void
 // ssd_scan_fwd_chunk.hip (bf16 with 16-byte vector access): one block per (chunk, head slice)
 bool scan_fwd_chunk_supported(int dtype, const SsdDims& d);
 size_t lds_scan_fwd_chunk(const SsdDims& d);
-hipError_t launch_scan_fwd_chunk(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s);
+// with `fast` (the k_chunk_cumsum flags) only slices holding a flagged (chunk, head) run: the fixup
+// of the factorised kernel
+hipError_t launch_scan_fwd_chunk(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, const int32_t* fast,
+                                 hipStream_t s);
+
+// ssd_scan_fwd_fact.hip (same shapes): the factorised-decay forward scan, exact for the (chunk, head)
+// pairs k_chunk_cumsum flags 1; the others are rewritten by launch_scan_fwd_chunk(..., b.fast, ...)
+size_t lds_scan_fwd_fact(const SsdDims& d);
+hipError_t launch_scan_fwd_fact(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s);
 
 // ssd_scan_fwd.hip
 hipError_t launch_chunk_scan_fwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,

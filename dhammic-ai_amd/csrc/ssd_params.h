@@ -24,6 +24,8 @@ struct SsdBufs {
   ChunkInfo* chunks;       // [max_chunks]
   int32_t* seq_chunk0;     // [nseq + 1] first chunk of each sequence
   float* cs;               // [max_chunks][H][Qpad] in-chunk inclusive cumsum of a
+  int32_t* fast;           // [max_chunks][H] 1: the factorised-decay kernels are exact enough
+                           // for this (chunk, head) (see k_chunk_cumsum), 0: exact-path fixup
   void* hin;               // [max_chunks][H][Ppad][Npad] (T) state entering each chunk
   void* ypre;              // [R][H][P] (T) y before the gated norm (has_z)
   float* rstd;             // [R] (has_z)

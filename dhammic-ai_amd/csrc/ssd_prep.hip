@@ -75,7 +75,8 @@ hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t*
 template <typename T>
 __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                       const void* __restrict__ Av, const float* __restrict__ dt,
-                                                      float* __restrict__ cs, T* __restrict__ acs_out) {
+                                                      float* __restrict__ cs, T* __restrict__ acs_out,
+                                                      int32_t* __restrict__ fast) {
   const int c = blockIdx.x;
   const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
@@ -121,6 +122,22 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
   }
   float* out = cs + ((int64_t)c * d.H + h) * d.Qpad;
   for (int e = 0; e < per; ++e) out[lane * per + e] = v[e];
+  if (fast) {
+    // Factorised-decay guard: cs non-increasing over the chunk (every a <= 0)
+    // and each 64-token block's drop cs[64 j] - cs[64 j + 63] at most
+    // SSD_FACT_RANGE, so exp(cs_l - c) and exp(c - cs_s) around a block-end
+    // reference c stay inside fp32 and bf16 (see the factorised kernels).
+    bool ok = true;
+    for (int e = 1; e < per; ++e) ok = ok && v[e] <= v[e - 1];
+    const float prev = __shfl_up(v[per - 1], 1, 64);
+    if (lane > 0) ok = ok && v[0] <= prev;
+    const int lpb = 64 / per;  // lanes per 64-token block
+    const int first = lane & ~(lpb - 1);
+    const float top = __shfl(v[0], first, 64), bot = __shfl(v[per - 1], first + lpb - 1, 64);
+    ok = ok && (top - bot) <= SSD_FACT_RANGE;
+    const bool all_ok = __all(ok);
+    if (lane == 0) fast[(int64_t)c * d.H + h] = all_ok ? 1 : 0;
+  }
   if (acs_out) {
     const int nch = d.seqlen / d.Q;
     T* o = acs_out + (((int64_t)ci.seq * d.H + h) * nch + ci.idx_in_seq) * d.Q;
@@ -136,10 +153,10 @@ hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, co
   dim3 grid(d.max_chunks, (d.H + 3) / 4);
   if (dtype == 1)
     hipLaunchKernelGGL(k_chunk_cumsum<bf16>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
-                       reinterpret_cast<bf16*>(A_cumsum_out));
+                       reinterpret_cast<bf16*>(A_cumsum_out), b.fast);
   else
     hipLaunchKernelGGL(k_chunk_cumsum<float>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
-                       reinterpret_cast<float*>(A_cumsum_out));
+                       reinterpret_cast<float*>(A_cumsum_out), b.fast);
   return hipGetLastError();
 }
 

@@ -19,6 +19,9 @@
 //   transposed in the accumulator's row order); Y_off^T = h_in C^T scaled by
 //   exp(clamp(cs_l)) per lane. The next head's x / h_in / cs / dt are loaded
 //   into registers while the current head computes.
+// This exact per-element form runs as the fixup of the factorised kernel
+// (ssd_scan_fwd_fact.hip): with `fast` given, only blocks whose head slice
+// holds a (chunk, head) flagged 0 run, and they rewrite their whole slice.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
 
@@ -49,7 +52,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict__ chunks, const float* __restrict__ cs,
                  const bf16* __restrict__ hin, const bf16* __restrict__ x, const float* __restrict__ dt,
                  const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const float* __restrict__ Dv,
-                 bf16* __restrict__ y) {
+                 bf16* __restrict__ y, const int32_t* __restrict__ fast) {
   constexpr int PP = 32 * PT, NP = 32 * NT;
   constexpr int XT = tsize<64, PP>(), CT = tsize<64, NP>();
   extern __shared__ __align__(16) unsigned char smem[];
@@ -62,6 +65,12 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
   const int h_lo = g * d.hpg + slc * hslice;
   const int h_hi = min(h_lo + hslice, (g + 1) * d.hpg);
   if (h_lo >= h_hi) return;
+  if (fast) {
+    // fixup mode: only slices holding a head the factorised kernel cannot take
+    bool need = false;
+    for (int h = h_lo + (int)threadIdx.x; h < h_hi; h += 256) need = need || fast[(int64_t)c * d.H + h] == 0;
+    if (!__syncthreads_or(need)) return;
+  }
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
   const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
@@ -246,7 +255,8 @@ size_t lds_scan_fwd_chunk(const SsdDims& d) {
 }
 
 template <int PT, int NT, int NB>
-static hipError_t scan_fwd_chunk_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+static hipError_t scan_fwd_chunk_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y,
+                                   const int32_t* fast, hipStream_t s) {
   // heads per block: about four blocks per CU over the grid
   const int per = d.max_chunks * d.G;
   int ns = (1024 + per - 1) / per;
@@ -259,27 +269,29 @@ static hipError_t scan_fwd_chunk_t(const SsdDims& d, const SsdBufs& b, const Ssd
   hipLaunchKernelGGL((k_scan_fwd_chunk<PT, NT, NB>), dim3(d.max_chunks * d.G * ns), dim3(256), lds, s, d, hslice, ns,
                      b.chunks, b.cs, reinterpret_cast<const bf16*>(b.hin), reinterpret_cast<const bf16*>(in.x), in.dt,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), in.D,
-                     reinterpret_cast<bf16*>(y));
+                     reinterpret_cast<bf16*>(y), fast);
   return hipGetLastError();
 }
 
 template <int PT, int NT>
-static hipError_t scan_fwd_chunk_nb(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+static hipError_t scan_fwd_chunk_nb(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y,
+                                    const int32_t* fast, hipStream_t s) {
   switch (d.Qpad / 64) {
-    case 1: return scan_fwd_chunk_t<PT, NT, 1>(d, b, in, y, s);
-    case 2: return scan_fwd_chunk_t<PT, NT, 2>(d, b, in, y, s);
-    case 3: return scan_fwd_chunk_t<PT, NT, 3>(d, b, in, y, s);
-    default: return scan_fwd_chunk_t<PT, NT, 4>(d, b, in, y, s);
+    case 1: return scan_fwd_chunk_t<PT, NT, 1>(d, b, in, y, fast, s);
+    case 2: return scan_fwd_chunk_t<PT, NT, 2>(d, b, in, y, fast, s);
+    case 3: return scan_fwd_chunk_t<PT, NT, 3>(d, b, in, y, fast, s);
+    default: return scan_fwd_chunk_t<PT, NT, 4>(d, b, in, y, fast, s);
   }
 }
 
-hipError_t launch_scan_fwd_chunk(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+hipError_t launch_scan_fwd_chunk(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, const int32_t* fast,
+                                 hipStream_t s) {
   switch (d.Ppad / 32 * 10 + d.Npad / 32) {
-    case 11: return scan_fwd_chunk_nb<1, 1>(d, b, in, y, s);
-    case 12: return scan_fwd_chunk_nb<1, 2>(d, b, in, y, s);
-    case 14: return scan_fwd_chunk_nb<1, 4>(d, b, in, y, s);
-    case 21: return scan_fwd_chunk_nb<2, 1>(d, b, in, y, s);
-    case 22: return scan_fwd_chunk_nb<2, 2>(d, b, in, y, s);
-    default: return scan_fwd_chunk_nb<2, 4>(d, b, in, y, s);
+    case 11: return scan_fwd_chunk_nb<1, 1>(d, b, in, y, fast, s);
+    case 12: return scan_fwd_chunk_nb<1, 2>(d, b, in, y, fast, s);
+    case 14: return scan_fwd_chunk_nb<1, 4>(d, b, in, y, fast, s);
+    case 21: return scan_fwd_chunk_nb<2, 1>(d, b, in, y, fast, s);
+    case 22: return scan_fwd_chunk_nb<2, 2>(d, b, in, y, fast, s);
+    default: return scan_fwd_chunk_nb<2, 4>(d, b, in, y, fast, s);
   }
 }

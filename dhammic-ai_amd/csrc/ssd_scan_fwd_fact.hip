@@ -1,0 +1,402 @@
+// Forward chunk scan with the factorised decay, bf16 inputs (gfx950).
+//
+// Per chunk and head (r2/dhammic-ai/src/kernels/ssd_scan.py:370-385 for the
+// intra-chunk term, :412-417 for the state term)
+//   Y[l] = sum_{s <= l} (C_l . B_s) exp(cs_l - cs_s) dt_s x_s + exp(clamp(cs_l)) C_l h_in^T + D x_l.
+// With c_j = cs at the last token of 64-token block j, every decay with s in
+// block j factorises as exp(cs_l - cs_s) = exp(cs_l - c_j) * exp(c_j - cs_s):
+//   X'_s   = dt_s exp(c_j - cs_s) x_s          (scaled once per head when x is staged)
+//   Y[l]  += exp(cs_l - c_j) * sum_{s in j, s <= l} S[l, s] X'_s,   S = C B^T,
+// so the causal S tiles are the MFMA operand as they are (computed once per
+// block, shared by its heads, causal mask applied once) and the decay costs one
+// multiply-add per output element and block j instead of an exp per (l, s)
+// pair. The reference clamps each exponent to [-20, 20]; the factorised form
+// is exact without the clamp, and for a non-increasing cs (every a <= 0) the
+// two differ only where cs_s - cs_l > 20, by at most e^-20 * sum |S X| per
+// output. Heads whose cs is not non-increasing, or drops by more than
+// SSD_FACT_RANGE inside one 64-token block (the factors would leave the
+// fp32/bf16 range), are flagged by k_chunk_cumsum and recomputed by the exact
+// kernel (k_scan_fwd_chunk in fixup mode) right after this one.
+//
+// One block per (chunk, group, slice of heads) with 4 waves per 32-wide p tile
+// (256 or 512 threads). Output Y^T[p][l] in 32-token quadrants (64-token block
+// i, half lh); wave w owns p tile w / 4 of two quadrants ({(3,1),(0,0)},
+// {(3,0),(0,1)}, {(2,1),(1,0)}, {(2,0),(1,1)} for w % 4 = 0..3 at a full chunk)
+// and keeps their nine 32 x 32 units S^T[s][l] in registers as bf16 B
+// operands. With two p tiles the block runs two waves per SIMD, so one wave's
+// LDS-read -> MFMA chain overlaps the other's. A head's output goes through
+// LDS and is written as whole rows while the next head is staged. Each head's x / h_in / cs / dt
+// are loaded into registers while the previous head computes; its scale factors
+// are written to LDS at the end of the previous head.
+#include "ssd_launch.h"
+#include "ssd_tile.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kFactUnits = 9;  // S^T units per wave (full 256-token chunk)
+
+template <int PT, int NT>
+struct FactLds {
+  static constexpr int PP = 32 * PT, NP = 32 * NT;
+  // C tiles, then the x / h_in tiles (which first hold two B tiles while the S units are built)
+  // C tiles, the x / h_in region, the output rows of one head, then cs and the two row-scale sets
+  static size_t bytes(int nb) {
+    const size_t xh = std::max<size_t>(nb * tsize<64, PP>() + tsize<PP, NP>(), 2 * tsize<64, NP>());
+    return 2 * (nb * tsize<64, NP>() + xh + nb * tsize<64, PP>()) + sizeof(float) * 3 * 64 * nb;
+  }
+  static constexpr int xh_elems(int nb) {
+    return nb * tsize<64, PP>() + tsize<PP, NP>() > 2 * tsize<64, NP>() ? nb * tsize<64, PP>() + tsize<PP, NP>()
+                                                                          : 2 * tsize<64, NP>();
+  }
+};
+
+template <int PT, int NT, int NB>
+struct FactStage {
+  static constexpr int NTHR = 256 * PT;
+  TileStage<64, 32 * PT, NTHR> x[NB];
+  TileStage<32 * PT, 32 * NT, NTHR> hin;
+  float cs, dt;
+};
+
+// Row-major staged tile to LDS with every row r scaled by sc[r] (fp32) before rounding.
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_store_scaled(const TileStage<ROWS, W, NTHR>& s, bf16* t,
+                                                    const float* __restrict__ sc) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      const float f = sc[r];
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * f);
+      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = o;
+    }
+  }
+}
+
+}  // namespace
+
+// Quadrants of quadrant-pair Wq = w % 4 (slot 0, slot 1; i = -1: none) for a chunk of NB
+// 64-token blocks: slot 0 = (NB-1-Wq/2, 1-Wq%2), slot 1 = (Wq/2, Wq%2) while Wq/2 < NB-2
+// (beyond that slot 0 of another pair holds it). A quadrant (i, lh) needs the 2 i + lh + 1
+// units (j, sh) <= (i, lh).
+template <int NB, int Wq> struct FactQuads {
+  static constexpr int i0 = (NB - 1) - Wq / 2, lh0 = 1 - Wq % 2;
+  static constexpr int i1 = (Wq / 2 < NB - 2) ? Wq / 2 : -1, lh1 = Wq % 2;
+  static constexpr int n0 = i0 >= 0 ? 2 * i0 + lh0 + 1 : 0;
+  static constexpr int n1 = i1 >= 0 ? 2 * i1 + lh1 + 1 : 0;
+  static constexpr int nU = n0 + n1;
+};
+
+template <int PT, int NT, int NB>
+struct FactCtx {
+  SsdDims d;
+  int hslice, nslices;
+  const ChunkInfo* chunks;
+  const float* cs;
+  const bf16* hin;
+  const bf16* x;
+  const float* dt;
+  const bf16* Bm;
+  const bf16* Cm;
+  const float* Dv;
+  bf16* y;
+};
+
+// The per-wave body: everything from the S units on, with the wave's quadrants,
+// units and p tile (pt) known at compile time. Block-wide barriers are reached
+// by every wave the same number of times.
+template <int PT, int NT, int NB, int Wq, int pt>
+__device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned char* smem, int c, const ChunkInfo& ci,
+                                          int g, int h_lo, int h_hi) {
+  constexpr int PP = 32 * PT, NP = 32 * NT, NTHR = 256 * PT;
+  constexpr int XT = tsize<64, PP>(), CT = tsize<64, NP>();
+  using QD = FactQuads<NB, Wq>;
+  constexpr int NU = QD::nU > 0 ? QD::nU : 1;
+  const SsdDims& d = a.d;
+  int lane = threadIdx.x & 63;
+  const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
+  bf16* Ct = reinterpret_cast<bf16*>(smem);
+  bf16* xt = Ct + NB * CT;
+  bf16* ht = xt + NB * XT;
+  bf16* ot = xt + FactLds<PT, NT>::xh_elems(NB);  // [64 NB][PP]: y rows of one head
+  float* s_cs2 = reinterpret_cast<float*>(ot + NB * XT);
+  float* s_g = s_cs2 + 64 * NB;
+  // y rows of head h from ot, whole 16-byte pieces of full rows per wave (coalesced lines)
+  auto store_out = [&](int h) {
+    constexpr int CPR = PP / 8;
+#pragma unroll
+    for (int q = 0; q < 64 * NB * CPR / NTHR; ++q) {
+      const int id = threadIdx.x + q * NTHR;
+      const int r = id / CPR, k = (id % CPR) * 8;
+      if (r < ci.len && k < d.P)
+        *reinterpret_cast<bf16x8*>(a.y + (int64_t)(ci.row0 + r) * xrow + (int64_t)h * d.P + k) = tld8<PP>(ot, r, k);
+    }
+  };
+
+  // ---- S^T units: rows s (block j half sh), lanes l (quadrant); causal mask on each diagonal unit.
+  // The B tiles go through the x / h_in region (free until the head loop), two blocks per round,
+  // so every global load of a round is in flight at once.
+  bf16x8 S[NU][2];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      S[u][0][e] = (bf16)0.0f;
+      S[u][1][e] = (bf16)0.0f;
+    }
+  }
+  bf16* Bt = xt;
+#pragma unroll
+  for (int r = 0; r < (NB + 1) / 2; ++r) {
+    if (r > 0) __syncthreads();  // the previous round's B reads are done
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int j = 2 * r + t;
+      if (j < NB) {
+        TileStage<64, NP, NTHR> sb;
+        tstage_load_v(sb, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
+                      min(64, ci.len - 64 * j), d.N);
+        tstage_store<64, NP, NTHR>(sb, Bt + t * CT);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < QD::nU; ++u) {
+      const int q = u < QD::n0 ? 0 : 1;
+      const int uu = q == 0 ? u : u - QD::n0;
+      const int qi = q == 0 ? QD::i0 : QD::i1, qlh = q == 0 ? QD::lh0 : QD::lh1;
+      const int j = uu >> 1, sh = uu & 1;
+      if (j / 2 != r) continue;
+      floatx16 sacc;
+      zero(sacc);
+#pragma unroll
+      for (int kk = 0; kk < NP; kk += 16) {
+        const int n0 = kk + 8 * (lane >> 5);
+        mfma(sacc, tld8<NP>(Bt + (j - 2 * r) * CT, 32 * sh + (lane & 31), n0),
+             tld8<NP>(Ct + qi * CT, 32 * qlh + (lane & 31), n0));
+      }
+      if (uu == (q == 0 ? QD::n0 : QD::n1) - 1) {  // diagonal unit: s > l is outside the causal mask
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (acc_row(v, lane) > (lane & 31)) sacc[v] = 0.0f;
+      }
+      S[u][0] = acc_frag(sacc, 0);
+      S[u][1] = acc_frag(sacc, 1);
+    }
+  }
+
+  // ---- per-head loop: the next head's inputs are loaded into registers while one head computes ----
+  FactStage<PT, NT, NB> st;
+  auto load_head = [&](int h) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      tstage_load_v(st.x[i], a.x + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
+                    min(64, ci.len - 64 * i), d.P);
+    tstage_load_v(st.hin, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    st.cs = 0.0f;
+    st.dt = 1.0f;
+    if (threadIdx.x < 64 * NB) {
+      st.cs = a.cs[((int64_t)c * d.H + h) * d.Qpad + threadIdx.x];
+      if (d.has_dt && (int)threadIdx.x < ci.len) st.dt = a.dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
+    }
+  };
+  // row scale of token t = threadIdx.x: dt_t * exp(c_j - cs_t); the wave's 64
+  // tokens are block j, whose last token is lane 63
+  auto put_g = [&](int buf) {
+    const float c2 = st.cs * SSD_LOG2E;
+    const float cj = __shfl(c2, 63, 64);
+    if (threadIdx.x < 64 * NB) s_g[buf * 64 * NB + threadIdx.x] = st.dt * exp2_fast(cj - c2);
+  };
+  load_head(h_lo);
+  put_g(0);
+  for (int h = h_lo; h < h_hi; ++h) {
+    const int buf = (h - h_lo) & 1;
+    lane = opaque_lane();
+    __syncthreads();  // the previous head's LDS reads are done; s_g[buf] is complete
+    if (h > h_lo) store_out(h - 1);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) tstage_store_scaled(st.x[i], xt + i * XT, s_g + buf * 64 * NB + 64 * i);
+    tstage_store<PP, NP, NTHR>(st.hin, ht);
+    if (threadIdx.x < 64 * NB) s_cs2[threadIdx.x] = st.cs * SSD_LOG2E;
+    __syncthreads();
+    // x_l (unscaled) of both quadrants for + D x, in the accumulator's p order. Issued
+    // before the next head's loads: vector-memory counters retire in order, so the
+    // epilogue's wait for these does not wait for the prefetch.
+    bf16x4 xv[2][4];
+    {
+      const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (int64_t)ci.row0 * xrow + (int64_t)h * d.P);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int i = q == 0 ? QD::i0 : QD::i1, lh = q == 0 ? QD::lh0 : QD::lh1;
+        const int lg = 64 * i + 32 * lh + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p0 = 32 * pt + 8 * r + 4 * (lane >> 5);
+          const bool ok = (q == 0 ? QD::n0 : QD::n1) > 0 && d.has_D && lg < ci.len && p0 < d.P;
+          xv[q][r] = __builtin_bit_cast(
+              bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rx, ok ? (int)(((int64_t)lg * xrow + p0) * 2) : SSD_BUF_SIZE,
+                                                           0, 0));
+        }
+      }
+    }
+    if (h + 1 < h_hi) load_head(h + 1);
+    const float Dh = d.has_D ? a.Dv[h] : 0.0f;
+
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = q == 0 ? QD::i0 : QD::i1, lh = q == 0 ? QD::lh0 : QD::lh1;
+      const int nq = q == 0 ? QD::n0 : QD::n1, base = q == 0 ? 0 : QD::n0;
+      if (nq == 0) continue;
+      const int l_loc = 32 * lh + (lane & 31);  // lane's token within block i
+      const int lg = 64 * i + l_loc;
+      const float cs_l = s_cs2[lg];
+      // Y_diag^T[p][l] = sum_j exp(cs_l - c_j) sum_{s in j} X'^T[p][s] S^T[s][l], accumulated
+      // Horner-wise from j = 0: acc = acc * exp(c_j - c_{j-1}) + T_j, then * exp(cs_l - c_i)
+      floatx16 acc;
+      zero(acc);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        if (u < base || u >= base + nq) continue;
+        const int uu = u - base;
+        const int j = uu >> 1, sh = uu & 1;
+        if (sh == 0 && j > 0) {
+          const float gam = exp2_fast(s_cs2[64 * j + 63] - s_cs2[64 * j - 1]);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[v] *= gam;
+        }
+        const bf16* xj = xt + j * XT;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) mfma(acc, ttr_perm<PP>(xj, 32 * sh, kk, 32 * pt, lane), S[u][kk]);
+      }
+      // acc * exp(cs_l - c_i) + exp(clamp(cs_l)) h_in C^T: scale by exp(cs_l - c_i) / e_off,
+      // accumulate h_in C^T, scale by e_off in the epilogue
+      const float e_off = exp2_fast(clamp_med3(cs_l, -SSD_T2, SSD_T2));
+      const float pre = exp2_fast(cs_l - s_cs2[64 * i + 63]) / e_off;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[v] *= pre;
+#pragma unroll
+      for (int kk = 0; kk < NP; kk += 16)
+        mfma(acc, tld8<NP>(ht, 32 * pt + (lane & 31), kk + 8 * (lane >> 5)),
+             tld8<NP>(Ct + i * CT, l_loc, kk + 8 * (lane >> 5)));
+      // epilogue: * e_off, + D x, into the output rows (lane l writes 4 consecutive p per register group)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p0 = 32 * pt + 8 * r + 4 * (lane >> 5);
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (bf16)fmaf(acc[4 * r + e], e_off, Dh * (float)xv[q][r][e]);
+        *reinterpret_cast<bf16x4*>(ot + toff<PP>(lg, p0)) = o;
+      }
+    }
+    if (h + 1 < h_hi) put_g(buf ^ 1);
+  }
+  __syncthreads();
+  store_out(h_hi - 1);
+}
+
+template <int PT, int NT, int NB>
+__global__ void __launch_bounds__(256 * PT) __attribute__((amdgpu_waves_per_eu(PT, PT)))
+k_scan_fwd_fact(FactCtx<PT, NT, NB> a) {
+  constexpr int NP = 32 * NT, NTHR = 256 * PT;
+  constexpr int CT = tsize<64, NP>();
+  extern __shared__ __align__(16) unsigned char smem[];
+  const SsdDims& d = a.d;
+  const int c = blockIdx.x % d.max_chunks;
+  const int gsl = blockIdx.x / d.max_chunks;
+  const int g = gsl / a.nslices, slc = gsl % a.nslices;
+  const ChunkInfo ci = a.chunks[c];
+  if (ci.len == 0) return;
+  const int h_lo = g * d.hpg + slc * a.hslice;
+  const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
+  if (h_lo >= h_hi) return;
+  const int64_t brow = (int64_t)d.G * d.N;
+
+  // ---- C tiles of the chunk (rows past its length are zero) ----
+  bf16* Ct = reinterpret_cast<bf16*>(smem);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    TileStage<64, NP, NTHR> st;
+    tstage_load_v(st, a.Cm + (int64_t)(ci.row0 + 64 * i) * brow + (int64_t)g * d.N, brow, min(64, ci.len - 64 * i),
+                  d.N);
+    tstage_store<64, NP, NTHR>(st, Ct + i * CT);
+  }
+  __syncthreads();
+  switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
+    case 0: fact_body<PT, NT, NB, 0, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 1: fact_body<PT, NT, NB, 1, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 2: fact_body<PT, NT, NB, 2, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 3: fact_body<PT, NT, NB, 3, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 4: fact_body<PT, NT, NB, 0, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 5: fact_body<PT, NT, NB, 1, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 6: fact_body<PT, NT, NB, 2, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
+    default: fact_body<PT, NT, NB, 3, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
+  }
+}
+
+// Same shapes as k_scan_fwd_chunk.
+size_t lds_scan_fwd_fact(const SsdDims& d) {
+  const int nb = d.Qpad / 64;
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return FactLds<1, 1>::bytes(nb);
+    case 12: return FactLds<1, 2>::bytes(nb);
+    case 14: return FactLds<1, 4>::bytes(nb);
+    case 21: return FactLds<2, 1>::bytes(nb);
+    case 22: return FactLds<2, 2>::bytes(nb);
+    default: return FactLds<2, 4>::bytes(nb);
+  }
+}
+
+template <int PT, int NT, int NB>
+static hipError_t scan_fwd_fact_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+  // heads per block: about four blocks per CU over the grid
+  const int per = d.max_chunks * d.G;
+  int ns = (1024 + per - 1) / per;
+  if (ns < 1) ns = 1;
+  if (ns > d.hpg) ns = d.hpg;
+  const int hslice = (d.hpg + ns - 1) / ns;
+  ns = (d.hpg + hslice - 1) / hslice;
+  const size_t lds = FactLds<PT, NT>::bytes(NB);
+  FactCtx<PT, NT, NB> a;
+  a.d = d;
+  a.hslice = hslice;
+  a.nslices = ns;
+  a.chunks = b.chunks;
+  a.cs = b.cs;
+  a.hin = reinterpret_cast<const bf16*>(b.hin);
+  a.x = reinterpret_cast<const bf16*>(in.x);
+  a.dt = in.dt;
+  a.Bm = reinterpret_cast<const bf16*>(in.B);
+  a.Cm = reinterpret_cast<const bf16*>(in.C);
+  a.Dv = in.D;
+  a.y = reinterpret_cast<bf16*>(y);
+  ensure_lds(k_scan_fwd_fact<PT, NT, NB>, lds);
+  hipLaunchKernelGGL((k_scan_fwd_fact<PT, NT, NB>), dim3(d.max_chunks * d.G * ns), dim3(256 * PT), lds, s, a);
+  return hipGetLastError();
+}
+
+template <int PT, int NT>
+static hipError_t scan_fwd_fact_nb(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+  switch (d.Qpad / 64) {
+    case 1: return scan_fwd_fact_t<PT, NT, 1>(d, b, in, y, s);
+    case 2: return scan_fwd_fact_t<PT, NT, 2>(d, b, in, y, s);
+    case 3: return scan_fwd_fact_t<PT, NT, 3>(d, b, in, y, s);
+    default: return scan_fwd_fact_t<PT, NT, 4>(d, b, in, y, s);
+  }
+}
+
+hipError_t launch_scan_fwd_fact(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void* y, hipStream_t s) {
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return scan_fwd_fact_nb<1, 1>(d, b, in, y, s);
+    case 12: return scan_fwd_fact_nb<1, 2>(d, b, in, y, s);
+    case 14: return scan_fwd_fact_nb<1, 4>(d, b, in, y, s);
+    case 21: return scan_fwd_fact_nb<2, 1>(d, b, in, y, s);
+    case 22: return scan_fwd_fact_nb<2, 2>(d, b, in, y, s);
+    default: return scan_fwd_fact_nb<2, 4>(d, b, in, y, s);
+  }
+}

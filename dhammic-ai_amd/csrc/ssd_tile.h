@@ -181,9 +181,15 @@ __device__ __forceinline__ void tstage_store(const TileStage<ROWS, W, NTHR>& s, 
 // ---------------------------------------------------------------------------
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define SSD_BUF_SIZE 0x7ffffff0
-// Resource over [base, base + SSD_BUF_SIZE) bytes; base must be wave-uniform.
+// Resource over [base, base + SSD_BUF_SIZE) bytes; base must be wave-uniform (it is
+// read from the first active lane, so the descriptor lives in scalar registers and the
+// loads need no per-lane descriptor loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, SSD_BUF_SIZE, 0x00020000);
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  void* u = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, SSD_BUF_SIZE, 0x00020000);
 }
 // 16 bytes at byte offset `off`, or zeros when `ok` is false.
 __device__ __forceinline__ bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int off, bool ok) {

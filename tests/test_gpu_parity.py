@@ -252,3 +252,25 @@ def test_backward_is_deterministic():
     for k in ("x", "dt", "A", "B", "C", "D", "z", "init"):
         assert torch.equal(r1[2][k], r2[2][k]), k
     assert torch.equal(r1[0], r2[0])
+
+
+def test_extended_bf16_exact_fixup_heads():
+    """Heads the factorised-decay kernels cannot take: a growing head (A > 0, so the
+    in-chunk cumsum is not non-increasing) and a head whose cumsum drops by far more
+    than the factorisation range inside one 64-token block (A = -400). Both go
+    through the exact fixup kernels; each head is checked on its own."""
+    shape = SsdShape(2, 1024, 8, 64, 1, 64, 256)
+    inp = _ext_inputs(shape, 16, torch.bfloat16, False)
+    inp["A"][1] = 0.05
+    inp["A"][5] = -400.0
+    out, fin, g = _run_ext(inp, shape, torch.bfloat16, False)
+    oo, fo, go = oracle_extended(inp, shape.chunk, init=inp["init"], dfinal=inp["dfinal"])
+    tol = TOL[torch.bfloat16]
+    for h in range(shape.nheads):
+        assert_close(f"out[h={h}]", out[:, :, h], oo[:, :, h], tol)
+        assert_close(f"dx[h={h}]", g["x"][:, :, h], go["x"][:, :, h], tol)
+        assert_close(f"ddt[h={h}]", g["dt"][:, :, h], go["dt"][:, :, h], tol)
+        assert_close(f"final[h={h}]", fin[:, h], fo[:, h], tol)
+        assert_close(f"dinit[h={h}]", g["init"][:, h], go["init"][:, h], tol)
+    for k in ("A", "D", "B", "C"):
+        assert_close("d" + k, g[k], go[k], tol)
