@@ -1,0 +1,453 @@
+// Fused backward of the chunked SSD scan with the factorised decay, bf16 inputs
+// (gfx950): the per-chunk work FusedSSDScan.backward
+// (r2/dhammic-ai/src/kernels/ssd_scan.py:467-533) gets by re-running the
+// forward under autograd.
+//
+// Per chunk, head h, 64-token column block j (tokens s) and row blocks i >= j
+// (tokens l), with c_j = cs at the last token of block j:
+//   L[l,s] = exp(cs_l - cs_s) = f_l g_s,   f_l = exp(cs_l - c_j),  g_s = exp(c_j - cs_s)
+//   X'_s   = dt_s g_s x_s,  dY'_l = f_l dy_l          (rows scaled once per head when staged)
+// so with S = C B^T (shared by the heads of a group):
+//   dS[l,s]   += dY'_l . X'_s                 (= dm dt L, summed over heads by the MFMA)
+//   dX_s       = g_s sum_l S[l,s] dY'_l + w_s B_s dst^T,   w_s = exp(clamp(cs_last - cs_s))
+//   G[l,s]     = S[l,s] (dY'_l . X'_s),  rowG_l = sum_s G[l,s],  colG_s = sum_l G[l,s]
+//   E_s        = pass(cs_last - cs_s) dt_s x_s . (w_s B_s dst^T),  xdx_s = x_s . dX_s
+//   dx_s       = dt_s dX_s + D dy_s
+// The reference clamps every decay exponent to [-20, 20] and masks the clamp's
+// gradient (:192, :230); for a non-increasing cs the factorised form differs
+// only where cs_s - cs_l > 20, by at most e^-20 times the magnitude of the
+// terms. (chunk, head) pairs outside the factorisation's range are flagged by
+// k_chunk_cumsum; here their scaled rows are zero (no dS contribution) and the
+// exact kernel (k_bwd_main in fixup mode) rewrites their outputs afterwards.
+//
+// One block (4 waves) per (column block j, chunk, group, head slice), heads in
+// sequence. S^T tiles (i, j) are built once per block: kept in registers (the
+// per-wave 32 x 32 quadrant, for rowG) and in LDS (the B operand of dX). Wave w
+// owns quadrant (s half w % 2, l half w / 2) of every tile for dS / rowG, and
+// dX^T tile (p tile w / 2, s half w % 2) over all l. The next head's inputs are
+// loaded into registers while a head computes; its row scales are written to
+// LDS at the end of the head; a head's dx rows and per-token sums go out
+// through LDS while the next head is staged.
+#include "ssd_launch.h"
+#include "ssd_tile.h"
+
+struct BwdFactArgs {
+  const ChunkInfo* chunks;
+  const float* cs;     // [MC][H][Qpad]
+  const int32_t* fast; // [MC][H]
+  const bf16* dst;     // [MC][H][Ppad][Npad], gradient leaving each chunk (bf16)
+  const bf16* x;
+  const float* dt;
+  const bf16* Bm;
+  const bf16* Cm;
+  const float* Dv;
+  const bf16* dy;
+  bf16* dx;
+  float* rowG;     // [nb][MC][H][Qpad], partial per column block
+  float* colG;     // [MC][H][Qpad]
+  float* eterm;
+  float* xdx;
+  float* dD_part;  // [MC][H][Qpad/64]
+  float* dS;       // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
+  int nslices, hslice;
+};
+
+namespace {
+
+constexpr int kSlots = 4;  // row blocks per column block (Qpad <= 256)
+
+template <int PT, int NT>
+struct BwdFactLds {
+  static constexpr int PP = 32 * PT, NP = 32 * NT;
+  static constexpr int XT = tsize<64, PP>(), SQ = tsize<64, 64>(), DT = tsize<PP, NP>(), BT = tsize<64, NP>();
+  static constexpr int RED = 1024;
+  // bf16: xs, xu, dyu, ot, dYs[4], St[4], dstT, Bt; fp32: cs2, dt, f, g (Qpad each), reductions
+  static size_t bytes(int Qpad) { return 2 * (size_t)(8 * XT + kSlots * SQ + DT + BT) + 4 * (size_t)(4 * Qpad + RED); }
+};
+
+template <int PT, int NT>
+struct BwdFactStage {
+  TileStage<64, 32 * PT, 256> x, y[kSlots];
+  TileStage<32 * PT, 32 * NT, 256> dst;
+  float cs, dt, cj;
+  int fast;
+};
+
+// Row-major staged tile to LDS with row r scaled by sc[r] (fp32) before rounding.
+template <int ROWS, int W, int NTHR>
+__device__ __forceinline__ void tstage_store_rs(const TileStage<ROWS, W, NTHR>& s, bf16* t,
+                                                const float* __restrict__ sc) {
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+    const int id = threadIdx.x + q * NTHR;
+    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+      const int r = id / CPR, k = (id % CPR) * 8;
+      const float f = sc[r];
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * f);
+      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = o;
+    }
+  }
+}
+
+}  // namespace
+
+template <int PT, int NT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_bwd_fact(SsdDims d, BwdFactArgs a) {
+  using LD = BwdFactLds<PT, NT>;
+  constexpr int PP = 32 * PT, NP = 32 * NT;
+  constexpr int XT = LD::XT, SQ = LD::SQ;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = d.Qpad / 64;
+
+  const int U = d.max_chunks * d.G * a.nslices;
+  const int U8 = (U + 7) / 8 * 8;
+  const int j = blockIdx.x / U8;
+  const int u = blockIdx.x % U8;
+  if (u >= U) return;
+  const int c = u % d.max_chunks;
+  const int gsl = u / d.max_chunks;
+  const int g = gsl / a.nslices, slc = gsl % a.nslices;
+  const ChunkInfo ci = a.chunks[c];
+  const int nbl = (ci.len + 63) >> 6;
+  if (j >= nbl) return;
+  const int nt_i = nbl - j;  // tiles (i, j), i = j .. nbl-1
+  const int h_lo = g * d.hpg + slc * a.hslice;
+  const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
+  if (h_lo >= h_hi) return;
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = w & 1, wc = w >> 1;  // dS / rowG quadrant: s half, l half
+  const int pt = w >> 1, sr = w & 1;  // dX^T tile: p tile, s half
+  int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
+  const int Qpad = d.Qpad;
+  const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
+
+  bf16* xs = reinterpret_cast<bf16*>(smem);  // X' rows of block j      [64][PP]
+  bf16* xu = xs + XT;                        // x rows of block j       [64][PP]
+  bf16* dyu = xu + XT;                       // dy rows of block j      [64][PP]
+  bf16* ot = dyu + XT;                       // dx rows of block j      [64][PP]
+  bf16* dYs = ot + XT;                       // dY' rows of blocks i    [4][64][PP]
+  bf16* St = dYs + kSlots * XT;              // S^T tiles (i, j)        [4][64 s][64 l]
+  bf16* dstT = St + kSlots * SQ;             // dst                     [PP][NP]
+  bf16* Bt = dstT + LD::DT;                  // B rows of block j       [64][NP]
+  float* s_cs2 = reinterpret_cast<float*>(Bt + LD::BT);  // cs * log2(e)  [Qpad]
+  float* s_dt = s_cs2 + Qpad;                             // dt            [Qpad]
+  float* s_f = s_dt + Qpad;   // next head's dY' row scales exp(cs_l - c_j) (0 for a flagged head)
+  float* s_g = s_f + Qpad;    // next head's X' row scales dt exp(c_j - cs_s) (block j tokens at 64 j ..)
+  float* red = s_g + Qpad;
+  float* red_row = red;        // [4 slots][2 wr][64]
+  float* red_col = red + 512;  // [2 wc][64]
+  float* red_e = red + 640;    // [2 pt][64]
+  float* red_x = red + 768;    // [2 pt][64]
+  float* red_d = red + 896;    // [4 waves]
+
+  // ---- B rows of block j; S^T tiles (i, j): rows s (block j), columns l (block i) ----
+  {
+    TileStage<64, NP, 256> st;
+    tstage_load_v(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
+                  min(64, ci.len - 64 * j), d.N);
+    tstage_store(st, Bt);
+  }
+  __syncthreads();
+  bf16x8 S[kSlots][2];
+#pragma unroll
+  for (int t = 0; t < kSlots; ++t) {
+    floatx16 sacc;
+    zero(sacc);
+    const int i = j + t;
+    if (t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
+      const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
+      const int lrow = 64 * i + 32 * wc + l32;
+      bf16x8 cb[NP / 16];
+#pragma unroll
+      for (int kk = 0; kk < NP / 16; ++kk) {
+        const int n0 = 16 * kk + 8 * hh;
+        cb[kk] = buf_ld16(rc, (int)(((int64_t)lrow * brow + n0) * 2), lrow < ci.len && n0 < d.N);
+      }
+#pragma unroll
+      for (int kk = 0; kk < NP / 16; ++kk) mfma(sacc, tld8<NP>(Bt, 32 * wr + l32, 16 * kk + 8 * hh), cb[kk]);
+      if (t == 0) {  // diagonal tile: s > l is outside the causal mask
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (32 * wr + acc_row(v, lane) > 32 * wc + l32) sacc[v] = 0.0f;
+      }
+    }
+    S[t][0] = acc_frag(sacc, 0);
+    S[t][1] = acc_frag(sacc, 1);
+    // LDS copy S^T[s][l] of the quadrant (also for tiles / quadrants that stay zero)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)sacc[v];
+  }
+
+  floatx16 dS[kSlots];
+#pragma unroll
+  for (int t = 0; t < kSlots; ++t) zero(dS[t]);
+
+  BwdFactStage<PT, NT> hs;
+  auto load_head = [&](int h) {
+    const int64_t xo = (int64_t)h * d.P;
+    tstage_load_v(hs.x, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
+#pragma unroll
+    for (int t = 0; t < kSlots; ++t)
+      if (t < nt_i)
+        tstage_load_v(hs.y[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + xo, xrow,
+                      min(64, ci.len - 64 * (j + t)), d.P);
+    tstage_load_v(hs.dst, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    const float* csh = a.cs + ((int64_t)c * d.H + h) * Qpad;
+    hs.cs = 0.0f;
+    hs.dt = 1.0f;
+    if ((int)threadIdx.x < Qpad) {
+      hs.cs = csh[threadIdx.x];
+      if (d.has_dt && (int)threadIdx.x < ci.len) hs.dt = a.dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
+    }
+    hs.cj = csh[64 * j + 63];
+    hs.fast = a.fast[(int64_t)c * d.H + h];
+  };
+  // row scales of the head in hs (token t = threadIdx.x): dY' rows exp(cs_t - c_j), X' rows
+  // dt_t exp(c_j - cs_t) for t in block j; zero for a flagged head
+  auto put_scales = [&]() {
+    if ((int)threadIdx.x < Qpad) {
+      const float c2 = hs.cs * SSD_LOG2E, cj2 = hs.cj * SSD_LOG2E;
+      const bool ok = hs.fast != 0;
+      s_f[threadIdx.x] = ok ? exp2_fast(c2 - cj2) : 0.0f;
+      s_g[threadIdx.x] = ok ? hs.dt * exp2_fast(cj2 - c2) : 0.0f;
+    }
+  };
+  // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
+  auto flush = [&](int h) {
+    const int64_t hq = ((int64_t)c * d.H + h) * Qpad;
+    if (threadIdx.x < 64) {
+      const int tl = threadIdx.x, tg = 64 * j + tl;
+      if (tg < ci.len) {
+        a.colG[hq + tg] = red_col[tl] + red_col[64 + tl];
+        a.eterm[hq + tg] = red_e[tl] + red_e[64 + tl];
+        a.xdx[hq + tg] = red_x[tl] + red_x[64 + tl];
+      }
+    }
+    for (int e = threadIdx.x; e < nt_i * 64; e += 256) {
+      const int t = e / 64, l = e % 64;
+      const int lg = 64 * (j + t) + l;
+      if (lg < ci.len)
+        a.rowG[((int64_t)j * d.max_chunks + c) * d.H * (int64_t)Qpad + (int64_t)h * Qpad + lg] =
+            red_row[(t * 2 + 0) * 64 + l] + red_row[(t * 2 + 1) * 64 + l];
+    }
+    if (threadIdx.x == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_d[0] + red_d[1] + red_d[2] + red_d[3];
+    constexpr int CPR = PP / 8;
+#pragma unroll
+    for (int q = 0; q < 64 * CPR / 256; ++q) {
+      const int id = threadIdx.x + 256 * q;
+      const int r = id / CPR, k = (id % CPR) * 8;
+      if (64 * j + r < ci.len && k < d.P)
+        *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + k) =
+            tld8<PP>(ot, r, k);
+    }
+  };
+
+  load_head(h_lo);
+  put_scales();
+  for (int h = h_lo; h < h_hi; ++h) {
+    lane = opaque_lane();
+    hh = lane >> 5;
+    l32 = lane & 31;
+    __syncthreads();  // previous head: LDS reads done, reductions and ot complete; s_f / s_g of this head
+    if (h > h_lo) flush(h - 1);
+    tstage_store_rs(hs.x, xs, s_g + 64 * j);
+    tstage_store(hs.x, xu);
+    tstage_store(hs.y[0], dyu);
+#pragma unroll
+    for (int t = 0; t < kSlots; ++t)
+      if (t < nt_i) tstage_store_rs(hs.y[t], dYs + t * XT, s_f + 64 * (j + t));
+    tstage_store(hs.dst, dstT);
+    if ((int)threadIdx.x < Qpad) {
+      s_cs2[threadIdx.x] = hs.cs * SSD_LOG2E;
+      s_dt[threadIdx.x] = hs.dt;
+    }
+    __syncthreads();
+    if (h + 1 < h_hi) load_head(h + 1);
+    const float Dh = d.has_D ? a.Dv[h] : 0.0f;
+
+    // ---- tiles (i, j): dS += X' dY'^T (quadrant), rowG from S * (X' dY'^T), dX^T += dY'^T S ----
+    floatx16 dXa;
+    zero(dXa);
+    float colacc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) colacc[v] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kSlots; ++t) {
+      if (t >= nt_i) continue;
+      const bf16* dyt = dYs + t * XT;
+      if (!(t == 0 && wr == 1 && wc == 0)) {
+        floatx16 tq;
+        zero(tq);
+#pragma unroll
+        for (int kk = 0; kk < PP / 16; ++kk) {
+          const bf16x8 av = tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh);
+          const bf16x8 bv = tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh);
+          mfma(dS[t], av, bv);
+          mfma(tq, av, bv);
+        }
+        // G over the quadrant: lane l holds column l, registers the s rows; row sums per
+        // lane, column sums per register (both from the same products, so that the
+        // chunk total of rowG - colG cancels as the reference's does)
+        float rs = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float gv = (float)S[t][v >> 3][v & 7] * tq[v];
+          rs += gv;
+          colacc[v] += gv;
+        }
+        rs += __shfl_xor(rs, 32, 64);
+        if (hh == 0) red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
+      } else if (hh == 0) {
+        red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
+      }
+      if (pt < PT) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh));
+      }
+    }
+    // ---- colG_s over this wave's l: sum over the lanes of each register ----
+    {
+      const float cg = half_reduce16(colacc, lane);
+      const int idx = (lane >> 1) & 15;
+      if ((lane & 1) == 0) red_col[wc * 64 + 32 * wr + 8 * (idx >> 2) + 4 * hh + (idx & 3)] = cg;
+    }
+    // ---- state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
+    floatx16 dXs;
+    zero(dXs);
+    if (pt < PT) {
+#pragma unroll
+      for (int kk = 0; kk < NP / 16; ++kk)
+        mfma(dXs, tld8<NP>(dstT, 32 * pt + l32, 16 * kk + 8 * hh), tld8<NP>(Bt, 32 * sr + l32, 16 * kk + 8 * hh));
+    }
+
+    // ---- per token s (lane) of block j: scale, sums, dx (waves past the p tiles add zeros) ----
+    if (pt >= PT) {
+      if (hh == 0) {
+        red_e[pt * 64 + 32 * sr + l32] = 0.0f;
+        red_x[pt * 64 + 32 * sr + l32] = 0.0f;
+      }
+      if (lane == 0) red_d[w] = 0.0f;
+    } else {
+      const int s_loc = 32 * sr + l32, sg = 64 * j + s_loc;
+      const float c2 = s_cs2[sg], cj2 = s_cs2[64 * j + 63], cl2 = s_cs2[Qpad - 1];
+      const float gs = exp2_fast(cj2 - c2);
+      const float dw = cl2 - c2;
+      const float ws = sg < ci.len ? exp2_fast(clamp_med3(dw, -SSD_T2, SSD_T2)) : 0.0f;
+      const float pw = fabsf(dw) < SSD_T2 ? 1.0f : 0.0f;
+      const float dts = s_dt[sg];
+      float esum = 0.0f, xsum = 0.0f, dsum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p0 = 32 * pt + 8 * r + 4 * hh;
+        const bf16x4 xv = tld4<PP>(xu, s_loc, p0);
+        const bf16x4 yv = tld4<PP>(dyu, s_loc, p0);
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * r + e;
+          const float xf = (float)xv[e], yf = (float)yv[e];
+          const float di = gs * dXa[v], ds = ws * dXs[v];
+          const float dX = di + ds;
+          esum = fmaf(xf, ds, esum);
+          xsum = fmaf(xf, dX, xsum);
+          dsum = fmaf(xf, yf, dsum);
+          o[e] = (bf16)fmaf(dts, dX, Dh * yf);
+        }
+        *reinterpret_cast<bf16x4*>(ot + toff<PP>(s_loc, p0)) = o;
+      }
+      esum += __shfl_xor(esum, 32, 64);
+      xsum += __shfl_xor(xsum, 32, 64);
+      for (int o2 = 32; o2 > 0; o2 >>= 1) dsum += __shfl_xor(dsum, o2, 64);
+      if (hh == 0) {
+        red_e[pt * 64 + s_loc] = esum * dts * pw;
+        red_x[pt * 64 + s_loc] = xsum;
+      }
+      if (lane == 0) red_d[w] = dsum;
+    }
+    if (h + 1 < h_hi) put_scales();
+  }
+  __syncthreads();
+  flush(h_hi - 1);
+
+  // ---- dS tiles, summed over the slice's heads (zero outside the causal mask) ----
+  float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
+#pragma unroll
+  for (int t = 0; t < kSlots; ++t) {
+    if (t >= nt_i) continue;
+    float* tile = dSbase + (int64_t)((j + t) * nb + j) * 4096;
+    const int l_loc = 32 * wc + l32;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatx4 q;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int s_loc = 32 * wr + 8 * r + 4 * hh + e;
+        q[e] = (t == 0 && s_loc > l_loc) ? 0.0f : dS[t][4 * r + e];
+      }
+      *reinterpret_cast<floatx4*>(tile + l_loc * 64 + 32 * wr + 8 * r + 4 * hh) = q;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: the same shapes and grid as k_bwd_main (ssd_bwd_main.hip).
+// ---------------------------------------------------------------------------
+size_t lds_bwd_fact(const SsdDims& d) {
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return BwdFactLds<1, 1>::bytes(d.Qpad);
+    case 12: return BwdFactLds<1, 2>::bytes(d.Qpad);
+    case 14: return BwdFactLds<1, 4>::bytes(d.Qpad);
+    case 21: return BwdFactLds<2, 1>::bytes(d.Qpad);
+    case 22: return BwdFactLds<2, 2>::bytes(d.Qpad);
+    default: return BwdFactLds<2, 4>::bytes(d.Qpad);
+  }
+}
+
+template <int PT, int NT>
+static hipError_t bwd_fact_t(const SsdDims& d, const BwdFactArgs& a, hipStream_t s) {
+  const int U = d.max_chunks * d.G * a.nslices;
+  const int blocks = (U + 7) / 8 * 8 * (d.Qpad / 64);
+  const size_t lds = BwdFactLds<PT, NT>::bytes(d.Qpad);
+  ensure_lds(k_bwd_fact<PT, NT>, lds);
+  hipLaunchKernelGGL((k_bwd_fact<PT, NT>), dim3(blocks), dim3(256), lds, s, d, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_fact(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+                           hipStream_t s) {
+  BwdFactArgs a;
+  a.chunks = b.chunks;
+  a.cs = b.cs;
+  a.fast = b.fast;
+  a.dst = b.dst16;
+  a.x = reinterpret_cast<const bf16*>(in.x);
+  a.dt = in.dt;
+  a.Bm = reinterpret_cast<const bf16*>(in.B);
+  a.Cm = reinterpret_cast<const bf16*>(in.C);
+  a.Dv = in.D;
+  a.dy = reinterpret_cast<const bf16*>(dy);
+  a.dx = reinterpret_cast<bf16*>(dx);
+  a.rowG = b.rowG;
+  a.colG = b.colG;
+  a.eterm = b.eterm;
+  a.xdx = b.xdx;
+  a.dD_part = b.dD_part;
+  a.dS = b.dS_tiles;
+  a.nslices = b.nslices;
+  a.hslice = b.hslice;
+  switch (d.Ppad / 32 * 10 + d.Npad / 32) {
+    case 11: return bwd_fact_t<1, 1>(d, a, s);
+    case 12: return bwd_fact_t<1, 2>(d, a, s);
+    case 14: return bwd_fact_t<1, 4>(d, a, s);
+    case 21: return bwd_fact_t<2, 1>(d, a, s);
+    case 22: return bwd_fact_t<2, 2>(d, a, s);
+    default: return bwd_fact_t<2, 4>(d, a, s);
+  }
+}

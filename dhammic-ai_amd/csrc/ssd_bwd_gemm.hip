@@ -84,6 +84,7 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
                                                   const bf16* __restrict__ hin, const bf16* __restrict__ dst,
                                                   const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
                                                   const float* __restrict__ dS, int nslices,
+                                                  const float* __restrict__ dS_fix, const int32_t* __restrict__ fast,
                                                   float* __restrict__ dcs_off, bf16* __restrict__ dB,
                                                   bf16* __restrict__ dC) {
   using Cfg = GemmCfg<PT, NT>;
@@ -239,6 +240,12 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const int nbl = (ci.len + 63) >> 6;
   const int64_t sstride = (int64_t)MC * d.G * nb * nb * 4096;
   const float* dSc = dS + ((int64_t)c * d.G + g) * nb * nb * 4096;
+  // heads of the group the factorised kernel left to the exact fixup: their dS is in dS_fix
+  bool slow = false;
+  if (fast)
+    for (int hq = h0 + (int)threadIdx.x; hq < h1; hq += 256) slow = slow || fast[(int64_t)c * d.H + hq] == 0;
+  const bool any_fix = __syncthreads_or(slow);
+  const float* dSf = dS_fix + ((int64_t)c * d.G + g) * nb * nb * 4096;
   for (int pass = 0; pass < 2; ++pass) {
     const int lo = pass == 0 ? 0 : kb, hi = pass == 0 ? kb : nbl - 1;
     for (int m = lo; m <= hi; ++m) {
@@ -252,6 +259,11 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
         for (int sl = 1; sl < nslices; ++sl) {
           s0 += *reinterpret_cast<const floatx4*>(src + sl * sstride + r * 64 + k);
           s1 += *reinterpret_cast<const floatx4*>(src + sl * sstride + r * 64 + k + 4);
+        }
+        if (any_fix) {
+          const float* fx = dSf + (ti * nb + tj) * 4096;
+          s0 += *reinterpret_cast<const floatx4*>(fx + r * 64 + k);
+          s1 += *reinterpret_cast<const floatx4*>(fx + r * 64 + k + 4);
         }
         bf16x8 v;
         v[0] = (bf16)s0[0]; v[1] = (bf16)s0[1]; v[2] = (bf16)s0[2]; v[3] = (bf16)s0[3];
@@ -328,7 +340,8 @@ static hipError_t bwd_gemm_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in
                      d, b.chunks, b.cs, in.dt, reinterpret_cast<const bf16*>(in.x),
                      reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(b.hin), b.dst16,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), b.dS_tiles,
-                     b.nslices, b.dcs_off, reinterpret_cast<bf16*>(dB), reinterpret_cast<bf16*>(dC));
+                     b.nslices, b.dS_fix, b.fast, b.dcs_off, reinterpret_cast<bf16*>(dB),
+                     reinterpret_cast<bf16*>(dC));
   return hipGetLastError();
 }
 

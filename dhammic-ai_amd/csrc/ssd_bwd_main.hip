@@ -46,6 +46,9 @@ struct BwdMainArgs {
   float* dD_part;     // [MC][H][Qpad/64]
   float* dS;          // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
   int nslices, hslice;
+  // fixup mode (non-null): only the heads flagged 0 here run (the factorised kernel
+  // cannot take them); the block skips the others and exits if it has none
+  const int32_t* fast;
 };
 
 constexpr int kMaxSlots = 4;  // tiles per column block (nb <= 4)
@@ -88,6 +91,14 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   const int h_lo = g * d.hpg + slc * a.hslice;
   const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
   if (h_lo >= h_hi) return;
+  // the next head this block runs at or after h (h_hi: none)
+  auto next_head = [&](int h) {
+    if (a.fast)
+      while (h < h_hi && a.fast[(int64_t)c * d.H + h] != 0) ++h;
+    return h;
+  };
+  const int h_first = next_head(h_lo);
+  if (h_first >= h_hi) return;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wr = w & 1, wc = w >> 1;
   int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
@@ -176,8 +187,9 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
         tstage_load_v(hs.y[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + (int64_t)h * d.P, xrow,
                       min(64, ci.len - 64 * (j + t)), d.P);
   };
-  load_tiles(h_lo);
-  for (int h = h_lo; h < h_hi; ++h) {
+  load_tiles(h_first);
+  for (int h = h_first; h < h_hi;) {
+    const int h_next = next_head(h + 1);
     lane = opaque_lane();
 #pragma unroll
     for (int t = 0; t < kMaxSlots; ++t) {
@@ -297,7 +309,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     }
     tstage_store(sd, dstT);
     __syncthreads();
-    if (h + 1 < h_hi) load_tiles(h + 1);
+    if (h_next < h_hi) load_tiles(h_next);
 
     // ---- per-token state terms of column block j (lane = token t_loc) ----
     const float cs_t = s_cs2[tg];
@@ -366,6 +378,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     if (lane == 0) red_o[w] = dpart;
     __syncthreads();
     if (threadIdx.x == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_o[0] + red_o[1] + red_o[2] + red_o[3];
+    h = h_next;
   }
 
   // ---- outputs summed over the slice's heads ----
@@ -417,7 +430,8 @@ static hipError_t bwd_main_t(const SsdDims& d, const BwdMainArgs& a, hipStream_t
   return hipGetLastError();
 }
 
-static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx) {
+static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+                                  bool fixup) {
   BwdMainArgs a;
   a.chunks = b.chunks;
   a.cs = b.cs;
@@ -434,15 +448,16 @@ static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdI
   a.eterm = b.eterm;
   a.xdx = b.xdx;
   a.dD_part = b.dD_part;
-  a.dS = b.dS_tiles;
-  a.nslices = b.nslices;
-  a.hslice = b.hslice;
+  a.dS = fixup ? b.dS_fix : b.dS_tiles;
+  a.nslices = fixup ? 1 : b.nslices;
+  a.hslice = fixup ? d.hpg : b.hslice;
+  a.fast = fixup ? b.fast : nullptr;
   return a;
 }
 
-hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx, bool fixup,
                            hipStream_t s) {
-  const BwdMainArgs a = make_main_args(d, b, in, dy, dx);
+  const BwdMainArgs a = make_main_args(d, b, in, dy, dx, fixup);
   switch (d.Ppad / 32 * 10 + d.Npad / 32) {
     case 11: return bwd_main_t<1, 1>(d, a, s);
     case 12: return bwd_main_t<1, 2>(d, a, s);

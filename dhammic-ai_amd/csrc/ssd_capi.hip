@@ -24,7 +24,8 @@ struct Plan {
   // byte offsets inside each workspace
   size_t o_chunks, o_seq0, o_cs, o_fast, o_hin, o_ypre, o_rstd, saved_bytes;
   size_t o_st, fwd_bytes;
-  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dst16, bwd_bytes;
+  size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dSf, o_dst16,
+      bwd_bytes;
   int fused_bwd, nrowg;
 };
 
@@ -71,7 +72,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
   if ((scan_fwd_chunk_supported(p->dtype, d) ? std::max(lds_scan_fwd_chunk(d), lds_scan_fwd_fact(d))
                                               : lds_chunk_scan_fwd(p->dtype, d)) > kMaxLds ||
-      (p->fused_bwd ? (lds_bwd_main(d) > kMaxLds || lds_bwd_gemm(d) > kMaxLds)
+      (p->fused_bwd ? (lds_bwd_main(d) > kMaxLds || lds_bwd_fact(d) > kMaxLds || lds_bwd_gemm(d) > kMaxLds)
                     : (lds_bwd_col(p->dtype, d) > kMaxLds || lds_bwd_row(p->dtype, d) > kMaxLds)))
     return SSD_ERR_UNSUPPORTED;
 
@@ -127,6 +128,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   const size_t nbq = (size_t)(d.Qpad / SSD_BLK);
   const bool tiles = p->fused_bwd;
   p->o_dS = tiles ? take((size_t)p->nslices * MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
+  p->o_dSf = tiles ? take(MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
   p->o_dst16 = tiles ? take(MC * H * PN * 2) : 0;
   p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
   p->bwd_bytes = off;
@@ -168,6 +170,7 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->dC_part = parts ? reinterpret_cast<float*>(s + p.o_dCp) : nullptr;
   const bool tiles = p.fused_bwd;
   b->dS_tiles = tiles ? reinterpret_cast<float*>(s + p.o_dS) : nullptr;
+  b->dS_fix = tiles ? reinterpret_cast<float*>(s + p.o_dSf) : nullptr;
   b->dst16 = tiles ? reinterpret_cast<bf16*>(s + p.o_dst16) : nullptr;
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
 }
@@ -322,7 +325,11 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   }
   if (fused) {
     // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
-    SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_main(d, b, in, dY, a->dx, s));
+    // factorised column kernel, then the exact one on the (chunk, head) pairs it cannot take
+    SSD_TRY(tm.begin(SSD_PH_BWD_COL));
+    SSD_TRY(launch_bwd_fact(d, b, in, dY, a->dx, s));
+    SSD_TRY(launch_bwd_main(d, b, in, dY, a->dx, true, s));
+    SSD_TRY(tm.end(SSD_PH_BWD_COL));
     SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_gemm(d, b, in, dY, a->dB, a->dC, s));
   } else {
     SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));

@@ -81,7 +81,13 @@ size_t lds_bwd_row(int dtype, const SsdDims& d);
 bool bwd_main_supported(int dtype, const SsdDims& d);
 size_t lds_bwd_main(const SsdDims& d);
 int bwd_main_num_sets(const SsdDims& d);
-hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
+// fixup: only the (chunk, head) pairs b.fast flags 0, dS into b.dS_fix (the exact path behind k_bwd_fact)
+hipError_t launch_bwd_main(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx, bool fixup,
+                           hipStream_t s);
+
+// ssd_bwd_fact.hip (same shapes and grid as k_bwd_main): the factorised-decay column kernel
+size_t lds_bwd_fact(const SsdDims& d);
+hipError_t launch_bwd_fact(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dx,
                            hipStream_t s);
 
 // ssd_bwd_gemm.hip (fused path): dB, dC and the Y_off part of the decay gradient

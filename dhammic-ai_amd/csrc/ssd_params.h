@@ -45,6 +45,7 @@ struct SsdBufs {
   float* dB_part;          // [nslices][R][G][N] (column / row kernels)
   float* dC_part;          // [nslices][R][G][N]
   float* dS_tiles;         // fused path: [nslices][max_chunks][G][nb*nb][64][64] head-summed dS
+  float* dS_fix;           // fused path: [max_chunks][G][nb*nb][64][64] dS of the heads the exact fixup runs
   float* dw_part;          // [norm_blocks][H*P]
   int npass_blk, nslices, hslice, norm_blocks;
   int fused_bwd;           // 1: k_bwd_main + k_bwd_gemm (bf16), 0: column / row kernels
