@@ -90,7 +90,14 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   using Cfg = GemmCfg<PT, NT>;
   constexpr int PP = Cfg::PP, NP = Cfg::NP, NTW = (NT + 1) / 2, NK = PP / 16;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int c = blockIdx.x, kb = blockIdx.y, g = blockIdx.z;
+  // block -> (chunk, 64-token block kb): the nb blocks of a chunk are consecutive in
+  // dispatch order and share an XCD (same index mod 8), so each head's h_in / dst
+  // tiles come from HBM once and from that XCD's L2 for the other blocks
+  const int nbq = d.Qpad / 64;
+  const int x8 = blockIdx.x & 7, rr = blockIdx.x >> 3;
+  const int kb = rr % nbq;
+  const int c = (rr / nbq) * 8 + x8, g = blockIdx.y;
+  if (c >= d.max_chunks) return;
   const ChunkInfo ci = chunks[c];
   if (64 * kb >= ci.len) return;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -336,7 +343,8 @@ template <int PT, int NT>
 static hipError_t bwd_gemm_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, const void* dy, void* dB, void* dC,
                              hipStream_t s) {
   ensure_lds(k_bwd_gemm<PT, NT>, GemmCfg<PT, NT>::bytes);
-  hipLaunchKernelGGL((k_bwd_gemm<PT, NT>), dim3(d.max_chunks, d.Qpad / 64, d.G), dim3(256), (GemmCfg<PT, NT>::bytes), s,
+  const int nbq = d.Qpad / 64;
+  hipLaunchKernelGGL((k_bwd_gemm<PT, NT>), dim3((d.max_chunks + 7) / 8 * 8 * nbq, d.G), dim3(256), (GemmCfg<PT, NT>::bytes), s,
                      d, b.chunks, b.cs, in.dt, reinterpret_cast<const bf16*>(in.x),
                      reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(b.hin), b.dst16,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), b.dS_tiles,
