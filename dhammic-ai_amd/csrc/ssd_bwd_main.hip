@@ -91,6 +91,12 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
   const int h_lo = g * d.hpg + slc * a.hslice;
   const int h_hi = min(h_lo + a.hslice, (g + 1) * d.hpg);
   if (h_lo >= h_hi) return;
+  if (a.fast) {
+    // fixup mode: blocks whose heads all took the factorised path leave at once
+    bool need = false;
+    for (int h = h_lo + (int)threadIdx.x; h < h_hi; h += 256) need = need || a.fast[(int64_t)c * d.H + h] == 0;
+    if (!__syncthreads_or(need)) return;
+  }
   // the next head this block runs at or after h (h_hi: none)
   auto next_head = [&](int h) {
     if (a.fast)
