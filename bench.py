@@ -73,7 +73,6 @@ def phase_models(nchunks):
     fin = b * H * P * N * 4                  # final state / dfinal / dinit (fp32)
     cs = nchunks * H * Q * 4                 # in-chunk cumsum, and each per-token fp32 vector
     dS = nchunks * G * (nb * (nb + 1) // 2) * 64 * 64 * 4   # head-summed dS tiles (fp32)
-    bcp = R * G * N * 4                      # dB state part / dC Y_off part (fp32)
     m = {
         "cumsum": (0, dt + cs),
         "fwd_pass": (R * H * 2 * N * P, x + bc + dt + cs + st16 + fin),
@@ -81,9 +80,11 @@ def phase_models(nchunks):
         "norm_fwd": (0, 3 * x + R * 4),
         "norm_bwd": (0, 5 * x + R * 4),
         "bwd_pass": (R * H * 2 * N * P, x + bc + cs + 2 * st16 + 2 * fin),
-        "bwd_col": (R * H * (2 * (Q + 1) * P + 6 * N * P),
-                    3 * x + 2 * bc + dt + cs + 2 * st16 + dS + 2 * bcp + ((nb + 1) / 2 + 4) * cs),
-        "bwd_row": (R * G * 2 * (Q + 1) * N, 4 * bc + dS + 2 * bcp),
+        # column kernel: dS and G from X' dY'^T, dX = S^T dY' + w B dst^T, dx, per-token sums
+        "bwd_col": (R * H * (2 * (Q + 1) * P + 2 * N * P),
+                    3 * x + 2 * bc + dt + cs + st16 + dS + ((nb + 1) / 2 + 3) * cs),
+        # GEMM kernel: dB / dC from dS and from the head-summed state terms, the Y_off decay term
+        "bwd_row": (R * (H * 4 * N * P + G * 2 * (Q + 1) * N), 2 * x + 2 * st16 + 4 * bc + dS + dt + 2 * cs),
         "bwd_finish": (0, ((nb + 1) / 2 + 5) * cs + 2 * dt),
     }
     return m

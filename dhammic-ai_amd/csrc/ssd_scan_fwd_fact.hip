@@ -220,31 +220,16 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
     lane = opaque_lane();
     __syncthreads();  // the previous head's LDS reads are done; s_g[buf] is complete
     if (h > h_lo) store_out(h - 1);
+    // the output rows start as x (for + D x): each thread rewrites exactly the ot
+    // vectors store_out just read (same row-major thread mapping), so no barrier
 #pragma unroll
-    for (int i = 0; i < NB; ++i) tstage_store_scaled(st.x[i], xt + i * XT, s_g + buf * 64 * NB + 64 * i);
+    for (int i = 0; i < NB; ++i) {
+      tstage_store_scaled(st.x[i], xt + i * XT, s_g + buf * 64 * NB + 64 * i);
+      tstage_store<64, PP, NTHR>(st.x[i], ot + i * XT);
+    }
     tstage_store<PP, NP, NTHR>(st.hin, ht);
     if (threadIdx.x < 64 * NB) s_cs2[threadIdx.x] = st.cs * SSD_LOG2E;
     __syncthreads();
-    // x_l (unscaled) of both quadrants for + D x, in the accumulator's p order. Issued
-    // before the next head's loads: vector-memory counters retire in order, so the
-    // epilogue's wait for these does not wait for the prefetch.
-    bf16x4 xv[2][4];
-    {
-      const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (int64_t)ci.row0 * xrow + (int64_t)h * d.P);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int i = q == 0 ? QD::i0 : QD::i1, lh = q == 0 ? QD::lh0 : QD::lh1;
-        const int lg = 64 * i + 32 * lh + (lane & 31);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int p0 = 32 * pt + 8 * r + 4 * (lane >> 5);
-          const bool ok = (q == 0 ? QD::n0 : QD::n1) > 0 && d.has_D && lg < ci.len && p0 < d.P;
-          xv[q][r] = __builtin_bit_cast(
-              bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rx, ok ? (int)(((int64_t)lg * xrow + p0) * 2) : SSD_BUF_SIZE,
-                                                           0, 0));
-        }
-      }
-    }
     if (h + 1 < h_hi) load_head(h + 1);
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
 
@@ -284,14 +269,17 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
       for (int kk = 0; kk < NP; kk += 16)
         mfma(acc, tld8<NP>(ht, 32 * pt + (lane & 31), kk + 8 * (lane >> 5)),
              tld8<NP>(Ct + i * CT, l_loc, kk + 8 * (lane >> 5)));
-      // epilogue: * e_off, + D x, into the output rows (lane l writes 4 consecutive p per register group)
+      // epilogue: * e_off, + D x (x from the output rows), into the output rows (lane l
+      // rewrites 4 consecutive p per register group)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int p0 = 32 * pt + 8 * r + 4 * (lane >> 5);
+        bf16x4* op = reinterpret_cast<bf16x4*>(ot + toff<PP>(lg, p0));
+        const bf16x4 xv = *op;
         bf16x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (bf16)fmaf(acc[4 * r + e], e_off, Dh * (float)xv[q][r][e]);
-        *reinterpret_cast<bf16x4*>(ot + toff<PP>(lg, p0)) = o;
+        for (int e = 0; e < 4; ++e) o[e] = (bf16)fmaf(acc[4 * r + e], e_off, Dh * (float)xv[e]);
+        *op = o;
       }
     }
     if (h + 1 < h_hi) put_g(buf ^ 1);
