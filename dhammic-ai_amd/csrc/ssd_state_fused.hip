@@ -80,6 +80,10 @@ __global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2,
   __shared__ __align__(16) bf16 tv[2][tsize<64, 32, VPI>()];
   __shared__ float coef[2][64];
   __shared__ float red[4];
+  // per-wave 32 x 32 bf16 tile between the accumulator layout and whole 64-byte row
+  // pieces of HBM: the state written at a chunk start, and (backward) h_in at its end
+  constexpr int TP = 40;  // row pitch (elements)
+  __shared__ __align__(16) bf16 s_tile[PT][32 * TP];
   // block -> (n tile, unit = (head, sequence)); the n tiles of a unit share an XCD
   const int NTn = d.Npad / 32;
   const int x8 = blockIdx.x & 7, rr = blockIdx.x >> 3;
@@ -141,7 +145,7 @@ __global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2,
   int k = 0, t0 = 0, buf = 0;
   floatx16 acc;
   zero(acc);
-  bf16 hin_v[16];
+  bf16x8 hin_v[2];  // this lane's two 8-element row pieces of h_in (rows (lane + 64 q) / 4)
   // one 64-token step on the inputs in (st, cf); refills them with the step three ahead
   auto step = [&](StateStage<PT>& st, StepCoef& cf) {
     const int c = chunk_of(k);
@@ -149,13 +153,20 @@ __global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2,
     const float tot = cf.tot;
     const int64_t soff = ((int64_t)c * d.H + h) * d.Ppad * d.Npad;
     if (t0 == 0) {
-      // state entering (forward) / gradient leaving (backward) chunk c
+      // state entering (forward) / gradient leaving (backward) chunk c: accumulator layout
+      // -> this wave's LDS tile -> 16-byte row pieces (16 rows x 64 bytes per store)
+      bf16* tw = s_tile[w];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t o = soff + (int64_t)(prow0 + acc_row(v, lane)) * d.Npad + n;
-        hst[o] = (bf16)run[v];
-        if (!FWD) hin_v[v] = hin_in[o];  // consumed at the end of the chunk
+      for (int v = 0; v < 16; ++v) tw[acc_row(v, lane) * TP + (lane & 31)] = (bf16)run[v];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
+        const int64_t o = soff + (int64_t)(prow0 + r) * d.Npad + 32 * nt + c8;
+        *reinterpret_cast<bf16x8*>(hst + o) = *reinterpret_cast<const bf16x8*>(tw + r * TP + c8);
+        if (!FWD) hin_v[q] = *reinterpret_cast<const bf16x8*>(hin_in + o);  // consumed at the end of the chunk
       }
+      __builtin_amdgcn_wave_barrier();
     }
     if (threadIdx.x < 64) {
       const int l = t0 + threadIdx.x;
@@ -176,9 +187,17 @@ __global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2,
       // end of chunk c
       const float dec = exp_clamp(tot);
       if (!FWD) {
+        bf16* th = s_tile[w];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
+          *reinterpret_cast<bf16x8*>(th + r * TP + c8) = hin_v[q];
+        }
+        __builtin_amdgcn_wave_barrier();
         float contrib = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hin_v[v];
+        for (int v = 0; v < 16; ++v) contrib += run[v] * (float)th[acc_row(v, lane) * TP + (lane & 31)];
+        __builtin_amdgcn_wave_barrier();
         contrib *= dec * clamp_pass(tot);
         for (int o = 32; o > 0; o >>= 1) contrib += __shfl_xor(contrib, o, 64);
         if (lane == 0) red[w] = contrib;
