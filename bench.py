@@ -2,13 +2,15 @@
 """SSD scan fwd+bwd throughput on one MI355X, with the dominant kernel's
 roofline and the reference CPU path timed on the host beside it.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--copy-probe]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--copy-probe] [--config 2]
 
 A step is one forward + backward of the fused chunked SSD scan over the
-1.3B-class layer: B=4, L=8192, H=64, P=64, G=1, N=128,
-chunk 256, bf16 x/B/C/z/dy, fp32 dt/A/D, + D*x and the gated RMSNorm
-epilogue. Inputs are synthetic (the configs' distributions), generated on the
-GPU and resident in HBM before timing starts. Prints one JSON line.
+1.3B-class layer (the default): B=4, L=8192, H=64, P=64,
+G=1, N=128, chunk 256, bf16 x/B/C/z/dy, fp32 dt/A/D, + D*x and the gated
+RMSNorm epilogue. --config 1 (130M-class layer) and --config 3 (packed
+varlen, initial and final states) time the other BASELINE shapes the same
+way. Inputs are synthetic (the configs' distributions), generated on the GPU
+and resident in HBM before timing starts. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -26,7 +28,35 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "dhammic-ai_amd"))
 
 METRIC = "SSD scan fwd+bwd Mtokens/s at 1.3B-layer shape + % of MFMA/HBM roofline"
-CFG = dict(batch=4, seqlen=8192, nheads=64, headdim=64, ngroups=1, dstate=128, chunk=256)
+CONFIGS = {
+    1: dict(batch=8, seqlen=2048, nheads=24, headdim=64, ngroups=1, dstate=128, chunk=256),
+    2: dict(batch=4, seqlen=8192, nheads=64, headdim=64, ngroups=1, dstate=128, chunk=256),
+    3: dict(batch=1, seqlen=65536, nheads=32, headdim=64, ngroups=8, dstate=64, chunk=256),
+}
+WORKLOAD = {
+    1: "config 1: 130M-class SSD layer fwd+bwd with D",
+    2: "config 2: 1.3B-class SSD layer fwd+bwd with D and gated RMSNorm",
+    3: "config 3: packed varlen SSD fwd+bwd (lengths U{512..8192}) with D, initial and final states",
+}
+CFG = dict(CONFIGS[2])
+CFG_ID = 2
+
+
+def gated():
+    return CFG_ID == 2
+
+
+def varlen_lengths(total=65536, lo=512, hi=8192, seed=3):
+    """Config 3's sequence lengths: U{lo..hi} drawn until they reach `total`,
+    the last one trimmed (the same draw as the parity tests' inputs)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    lens, acc = [], 0
+    while acc < total:
+        v = min(int(torch.randint(lo, hi + 1, (1,), generator=g)), total - acc)
+        lens.append(v)
+        acc += v
+    return lens
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, GB/s
 PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
@@ -51,7 +81,21 @@ def make_inputs(dev, seed=2):
         "w": torch.ones(H * P, device=dev, dtype=torch.float32),
         "dy": torch.randn(b, L, H, P, **kw).to(bf),
     }
+    if CFG_ID == 3:
+        lens = varlen_lengths()
+        cu = [0]
+        for v in lens:
+            cu.append(cu[-1] + v)
+        t["cu"] = torch.tensor(cu, dtype=torch.int32, device=dev)
+        t["init"] = torch.randn(len(lens), H, P, N, **kw) * 0.1
+        t["dfinal"] = torch.randn(len(lens), H, P, N, **kw)
     return t
+
+
+def num_chunks():
+    if CFG_ID == 3:
+        return sum(-(-v // CFG["chunk"]) for v in varlen_lengths())
+    return CFG["batch"] * -(-CFG["seqlen"] // CFG["chunk"])
 
 
 def phase_models(nchunks):
@@ -70,7 +114,8 @@ def phase_models(nchunks):
     bc = R * G * N * es         # B or C
     dt = R * H * 4
     st16 = nchunks * H * P * N * es          # hin or dst (bf16, one state per chunk and head)
-    fin = b * H * P * N * 4                  # final state / dfinal / dinit (fp32)
+    nseq = len(varlen_lengths()) if CFG_ID == 3 else b
+    fin = nseq * H * P * N * 4               # final state / dfinal / dinit (fp32)
     cs = nchunks * H * Q * 4                 # in-chunk cumsum, and each per-token fp32 vector
     dS = nchunks * G * (nb * (nb + 1) // 2) * 64 * 64 * 4   # head-summed dS tiles (fp32)
     m = {
@@ -110,7 +155,7 @@ def measured_traffic(kernel):
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-probe factor), or None."""
     import re
     f = ROOT / "profiles" / "ssd_config2_hbm_traffic.md"
-    if not f.exists():
+    if CFG_ID != 2 or not f.exists():
         return None
     for line in f.read_text().splitlines():
         m = re.match(r"^- traffic (\w+): (\d+) bytes", line)
@@ -128,16 +173,19 @@ def time_gpu(steps, warmup, probe=False):
     if probe:
         copy_probe(dev)
     t = make_inputs(dev)
-    cfg = S._Cfg(chunk=CFG["chunk"], a_mode=C_.SSD_A_PER_HEAD, nseq=CFG["batch"], varlen=False,
-                 state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=1e-6)
+    vl = CFG_ID == 3
+    cfg = S._Cfg(chunk=CFG["chunk"], a_mode=C_.SSD_A_PER_HEAD, nseq=len(t["init"]) if vl else CFG["batch"],
+                 varlen=vl, state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=1e-6)
+    z, w = (t["z"], t["w"]) if gated() else (None, None)
+    init, cu, dfin = (t["init"], t["cu"], t["dfinal"]) if vl else (None, None, None)
     NP = C_.SSD_NUM_PHASES
     EvArr = ctypes.c_void_p * (2 * NP)
 
     def one_step(ev_arr=None):
-        y, final, _, saved = S._forward(cfg, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["z"], t["w"],
-                                        None, None, ev_arr)
-        S._backward(cfg, saved, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["z"], t["w"], None, None,
-                    t["dy"], None, ev_arr)
+        y, final, _, saved = S._forward(cfg, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], z, w,
+                                        init, cu, ev_arr)
+        S._backward(cfg, saved, t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], z, w, init, cu,
+                    t["dy"], dfin, ev_arr)
         return y
 
     for _ in range(warmup):
@@ -176,7 +224,7 @@ def time_gpu(steps, warmup, probe=False):
             phases[name] = statistics.mean(vals)
     # the same event pairs bracket the fwd_scan / bwd kernels of every step; also
     # count chunks for the models
-    nchunks = CFG["batch"] * math.ceil(CFG["seqlen"] / CFG["chunk"])
+    nchunks = num_chunks()
     return ms_total / steps, wall / steps * 1e3, phases, nchunks
 
 
@@ -271,7 +319,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run one plain 1 GiB device copy first (counter calibration)")
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS),
+                    help="BASELINE config to time (2 = the headline shape)")
     a = ap.parse_args()
+    global CFG, CFG_ID
+    CFG, CFG_ID = dict(CONFIGS[a.config]), a.config
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); the SSD scan is sharded "
               "across GPUs by batch/heads with no communication, so N GPUs run N independent copies.",
@@ -286,14 +338,14 @@ def main():
         "metric": METRIC, "value": value, "unit": "Mtokens/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "config 2: 1.3B-class SSD layer fwd+bwd with D and gated RMSNorm", **CFG,
+        "config": {"workload": WORKLOAD[CFG_ID], **CFG,
                    "x_dtype": "bf16", "state_dtype": "fp32", "tokens_per_step": tokens},
         "roofline": rl,
         "kernels_ms": {k: round(v, 4) for k, v in phases.items()},
         "kernels_roofline": per_kernel,
         "wall_ms_per_step": wall_ms,
     }
-    if rank == 0 and not a.no_cpu_baseline:
+    if rank == 0 and not a.no_cpu_baseline and CFG_ID == 2:
         out["cpu_baseline"] = cpu_baseline()
     if rank == 0:
         print(json.dumps(out), flush=True)
