@@ -20,13 +20,18 @@
 // k_chunk_cumsum; here their scaled rows are zero (no dS contribution) and the
 // exact kernel (k_bwd_main in fixup mode) rewrites their outputs afterwards.
 //
-// One block (4 waves) per (column block j, chunk, group, head slice), heads in
-// sequence. S^T tiles (i, j) are built once per block: kept in registers (the
-// per-wave 32 x 32 quadrant, for rowG) and in LDS (the B operand of dX). Wave w
-// owns quadrant (s half w % 2, l half w / 2) of every tile for dS / rowG, and
-// dX^T tile (p tile w / 2, s half w % 2) over all l. The next head's inputs are
-// loaded into registers while a head computes; its row scales are written to
-// LDS at the end of the head; a head's dx rows and per-token sums go out
+// One block (8 waves) per (column block j, chunk, group, head slice), heads in
+// sequence. The LDS the block needs allows one block per CU, so its waves are
+// split into two roles that share each SIMD and overlap: waves 0-3 own quadrant
+// (s half w % 2, l half w / 2) of every tile (i, j) for dS and rowG (S^T kept in
+// their registers), waves 4-7 own dX^T tile (p tile (w - 4) / 2, s half w % 2)
+// over all l (S^T read from an LDS copy) and finish the head's tokens. S^T tiles
+// are built once per block. colG_s = X'_s . W_s with
+// W^T = dY'^T S, the same bf16 operands and products as rowG, so the chunk total
+// of rowG - colG cancels as the reference's does. The next head's inputs, and
+// cs / dt at the rows each thread stages and at the token it finishes, are
+// loaded into registers while a head computes; row scales are applied in
+// registers when the head is staged; a head's dx rows and per-token sums go out
 // through LDS while the next head is staged.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
@@ -55,38 +60,43 @@ struct BwdFactArgs {
 namespace {
 
 constexpr int kSlots = 4;  // row blocks per column block (Qpad <= 256)
+constexpr int kThreads = 512;
 
 template <int PT, int NT>
 struct BwdFactLds {
   static constexpr int PP = 32 * PT, NP = 32 * NT;
   static constexpr int XT = tsize<64, PP>(), SQ = tsize<64, 64>(), DT = tsize<PP, NP>(), BT = tsize<64, NP>();
   static constexpr int RED = 1024;
-  // bf16: xs, xu, dyu, ot, dYs[4], St[4], dstT, Bt; fp32: cs2, dt, f, g (Qpad each), reductions
-  static size_t bytes(int Qpad) { return 2 * (size_t)(8 * XT + kSlots * SQ + DT + BT) + 4 * (size_t)(4 * Qpad + RED); }
+  // bf16: xs, xu, dyu, ot, dYs[4], St[4], dstT, Bt; fp32: reductions
+  static size_t bytes(int) { return 2 * (size_t)(8 * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
 };
 
 template <int PT, int NT>
 struct BwdFactStage {
-  TileStage<64, 32 * PT, 256> x, y[kSlots];
-  TileStage<32 * PT, 32 * NT, 256> dst;
-  float cs, dt, cj;
+  using Rows = TileStage<64, 32 * PT, kThreads>;
+  static constexpr int PER = Rows::PER;  // 16-byte pieces (and rows) per thread of a 64-row tile
+  Rows x, y[kSlots];
+  TileStage<32 * PT, 32 * NT, kThreads> dst;
+  float rcs[kSlots][PER];  // cs at this thread's staged rows of blocks j + t
+  float rdt[PER];          // dt at its staged rows of block j
+  float ecs, edt;          // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
+  float cj, cl;            // cs at the last token of block j and of the chunk
   int fast;
 };
 
-// Row-major staged tile to LDS with row r scaled by sc[r] (fp32) before rounding.
-template <int ROWS, int W, int NTHR>
-__device__ __forceinline__ void tstage_store_rs(const TileStage<ROWS, W, NTHR>& s, bf16* t,
-                                                const float* __restrict__ sc) {
+// Row-major staged 64-row tile to LDS, the piece of pass q scaled by sc[q] (fp32) before rounding.
+template <int W, int NTHR>
+__device__ __forceinline__ void tstage_store_sc(const TileStage<64, W, NTHR>& s, bf16* t,
+                                                const float (&sc)[TileStage<64, W, NTHR>::PER]) {
   constexpr int CPR = W / 8;
 #pragma unroll
-  for (int q = 0; q < TileStage<ROWS, W, NTHR>::PER; ++q) {
+  for (int q = 0; q < TileStage<64, W, NTHR>::PER; ++q) {
     const int id = threadIdx.x + q * NTHR;
-    if (TileStage<ROWS, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<ROWS, W, NTHR>::NVEC) {
+    if (TileStage<64, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<64, W, NTHR>::NVEC) {
       const int r = id / CPR, k = (id % CPR) * 8;
-      const float f = sc[r];
       bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * f);
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * sc[q]);
       *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = o;
     }
   }
@@ -95,7 +105,7 @@ __device__ __forceinline__ void tstage_store_rs(const TileStage<ROWS, W, NTHR>& 
 }  // namespace
 
 template <int PT, int NT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(kThreads)
 k_bwd_fact(SsdDims d, BwdFactArgs a) {
   using LD = BwdFactLds<PT, NT>;
   constexpr int PP = 32 * PT, NP = 32 * NT;
@@ -120,8 +130,9 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   if (h_lo >= h_hi) return;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wr = w & 1, wc = w >> 1;  // dS / rowG quadrant: s half, l half
-  const int pt = w >> 1, sr = w & 1;  // dX^T tile: p tile, s half
+  const bool xrole = w >= 4;                    // dX / token waves (else dS / rowG waves)
+  const int wr = w & 1, wc = (w >> 1) & 1;      // dS / rowG quadrant: s half, l half
+  const int pt = (w >> 1) & 1, sr = w & 1;      // dX^T tile: p tile, s half
   int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
   const int Qpad = d.Qpad;
   const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
@@ -134,32 +145,27 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   bf16* St = dYs + kSlots * XT;              // S^T tiles (i, j)        [4][64 s][64 l]
   bf16* dstT = St + kSlots * SQ;             // dst                     [PP][NP]
   bf16* Bt = dstT + LD::DT;                  // B rows of block j       [64][NP]
-  float* s_cs2 = reinterpret_cast<float*>(Bt + LD::BT);  // cs * log2(e)  [Qpad]
-  float* s_dt = s_cs2 + Qpad;                             // dt            [Qpad]
-  float* s_f = s_dt + Qpad;   // next head's dY' row scales exp(cs_l - c_j) (0 for a flagged head)
-  float* s_g = s_f + Qpad;    // next head's X' row scales dt exp(c_j - cs_s) (block j tokens at 64 j ..)
-  float* red = s_g + Qpad;
+  float* red = reinterpret_cast<float*>(Bt + LD::BT);
   float* red_row = red;        // [4 slots][2 wr][64]
-  float* red_col = red + 512;  // [2 wc][64]
+  float* red_col = red + 512;  // [2 pt][64]
   float* red_e = red + 640;    // [2 pt][64]
   float* red_x = red + 768;    // [2 pt][64]
-  float* red_d = red + 896;    // [4 waves]
+  float* red_d = red + 896;    // [4 dX waves]
 
   // ---- B rows of block j; S^T tiles (i, j): rows s (block j), columns l (block i) ----
   {
-    TileStage<64, NP, 256> st;
+    TileStage<64, NP, kThreads> st;
     tstage_load_v(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
                   min(64, ci.len - 64 * j), d.N);
     tstage_store(st, Bt);
   }
   __syncthreads();
-  bf16x8 S[kSlots][2];
 #pragma unroll
   for (int t = 0; t < kSlots; ++t) {
     floatx16 sacc;
     zero(sacc);
     const int i = j + t;
-    if (t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
+    if (!xrole && t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
       const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
       const int lrow = 64 * i + 32 * wc + l32;
       bf16x8 cb[NP / 16];
@@ -176,19 +182,26 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           if (32 * wr + acc_row(v, lane) > 32 * wc + l32) sacc[v] = 0.0f;
       }
     }
-    S[t][0] = acc_frag(sacc, 0);
-    S[t][1] = acc_frag(sacc, 1);
-    // LDS copy S^T[s][l] of the quadrant (also for tiles / quadrants that stay zero)
+    // S^T[s][l] of the quadrant to LDS (also for tiles / quadrants that stay zero)
+    if (!xrole) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)sacc[v];
+      for (int v = 0; v < 16; ++v)
+        St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)sacc[v];
+    }
   }
 
   floatx16 dS[kSlots];
 #pragma unroll
   for (int t = 0; t < kSlots; ++t) zero(dS[t]);
 
-  BwdFactStage<PT, NT> hs;
+  using HS = BwdFactStage<PT, NT>;
+  constexpr int PER = HS::PER, RPP = kThreads / (PP / 8);  // rows of a staged tile per pass
+  HS hs;
+  // dt of token tok (< Qpad) of the chunk; 1 past its end or without dt
+  auto dt_at = [&](int h, int tok) {
+    const float v = a.dt[(int64_t)(ci.row0 + min(tok, ci.len - 1)) * d.H + h];
+    return (d.has_dt && tok < ci.len) ? v : 1.0f;
+  };
   auto load_head = [&](int h) {
     const int64_t xo = (int64_t)h * d.P;
     tstage_load_v(hs.x, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
@@ -199,24 +212,19 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
                       min(64, ci.len - 64 * (j + t)), d.P);
     tstage_load_v(hs.dst, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
     const float* csh = a.cs + ((int64_t)c * d.H + h) * Qpad;
-    hs.cs = 0.0f;
-    hs.dt = 1.0f;
-    if ((int)threadIdx.x < Qpad) {
-      hs.cs = csh[threadIdx.x];
-      if (d.has_dt && (int)threadIdx.x < ci.len) hs.dt = a.dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
-    }
+    const int r0 = min((int)threadIdx.x / (PP / 8), 63);
+#pragma unroll
+    for (int t = 0; t < kSlots; ++t)
+#pragma unroll
+      for (int q = 0; q < PER; ++q) hs.rcs[t][q] = t < nt_i ? csh[64 * (j + t) + min(r0 + RPP * q, 63)] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) hs.rdt[q] = d.has_dt ? dt_at(h, 64 * j + min(r0 + RPP * q, 63)) : 1.0f;
+    const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);
+    hs.ecs = csh[te];
+    hs.edt = d.has_dt ? dt_at(h, te) : 1.0f;
     hs.cj = csh[64 * j + 63];
+    hs.cl = csh[Qpad - 1];
     hs.fast = a.fast[(int64_t)c * d.H + h];
-  };
-  // row scales of the head in hs (token t = threadIdx.x): dY' rows exp(cs_t - c_j), X' rows
-  // dt_t exp(c_j - cs_t) for t in block j; zero for a flagged head
-  auto put_scales = [&]() {
-    if ((int)threadIdx.x < Qpad) {
-      const float c2 = hs.cs * SSD_LOG2E, cj2 = hs.cj * SSD_LOG2E;
-      const bool ok = hs.fast != 0;
-      s_f[threadIdx.x] = ok ? exp2_fast(c2 - cj2) : 0.0f;
-      s_g[threadIdx.x] = ok ? hs.dt * exp2_fast(cj2 - c2) : 0.0f;
-    }
   };
   // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
   auto flush = [&](int h) {
@@ -229,7 +237,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         a.xdx[hq + tg] = red_x[tl] + red_x[64 + tl];
       }
     }
-    for (int e = threadIdx.x; e < nt_i * 64; e += 256) {
+    for (int e = threadIdx.x; e < nt_i * 64; e += kThreads) {
       const int t = e / 64, l = e % 64;
       const int lg = 64 * (j + t) + l;
       if (lg < ci.len)
@@ -239,8 +247,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     if (threadIdx.x == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_d[0] + red_d[1] + red_d[2] + red_d[3];
     constexpr int CPR = PP / 8;
 #pragma unroll
-    for (int q = 0; q < 64 * CPR / 256; ++q) {
-      const int id = threadIdx.x + 256 * q;
+    for (int id = threadIdx.x; id < 64 * CPR; id += kThreads) {
       const int r = id / CPR, k = (id % CPR) * 8;
       if (64 * j + r < ci.len && k < d.P)
         *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + k) =
@@ -249,105 +256,108 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   };
 
   load_head(h_lo);
-  put_scales();
   for (int h = h_lo; h < h_hi; ++h) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
-    __syncthreads();  // previous head: LDS reads done, reductions and ot complete; s_f / s_g of this head
+    __syncthreads();  // previous head: LDS reads done, reductions and ot complete
     if (h > h_lo) flush(h - 1);
-    tstage_store_rs(hs.x, xs, s_g + 64 * j);
+    // row scales (zero for a flagged head): X' rows dt_s exp(c_j - cs_s), dY' rows exp(cs_l - c_j)
+    {
+      const bool ok = hs.fast != 0;
+      const float cj2 = hs.cj * SSD_LOG2E;
+      float sc[PER];
+#pragma unroll
+      for (int q = 0; q < PER; ++q) sc[q] = ok ? hs.rdt[q] * exp2_fast(cj2 - hs.rcs[0][q] * SSD_LOG2E) : 0.0f;
+      tstage_store_sc(hs.x, xs, sc);
+#pragma unroll
+      for (int t = 0; t < kSlots; ++t)
+        if (t < nt_i) {
+#pragma unroll
+          for (int q = 0; q < PER; ++q) sc[q] = ok ? exp2_fast(hs.rcs[t][q] * SSD_LOG2E - cj2) : 0.0f;
+          tstage_store_sc(hs.y[t], dYs + t * XT, sc);
+        }
+    }
     tstage_store(hs.x, xu);
     tstage_store(hs.y[0], dyu);
-#pragma unroll
-    for (int t = 0; t < kSlots; ++t)
-      if (t < nt_i) tstage_store_rs(hs.y[t], dYs + t * XT, s_f + 64 * (j + t));
     tstage_store(hs.dst, dstT);
-    if ((int)threadIdx.x < Qpad) {
-      s_cs2[threadIdx.x] = hs.cs * SSD_LOG2E;
-      s_dt[threadIdx.x] = hs.dt;
-    }
+    // this head's per-token values for the finishing step (hs is reloaded below)
+    const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = hs.edt;
+    const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
     __syncthreads();
     if (h + 1 < h_hi) load_head(h + 1);
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
 
-    // ---- tiles (i, j): dS += X' dY'^T (quadrant), rowG from S * (X' dY'^T), dX^T += dY'^T S ----
-    floatx16 dXa;
-    zero(dXa);
-    float colacc[16];
+    if (!xrole) {
+      // ---- tiles (i, j): dS += X' dY'^T (quadrant), rowG from S * (X' dY'^T) ----
 #pragma unroll
-    for (int v = 0; v < 16; ++v) colacc[v] = 0.0f;
+      for (int t = 0; t < kSlots; ++t) {
+        if (t >= nt_i) continue;
+        const bf16* dyt = dYs + t * XT;
+        if (!(t == 0 && wr == 1 && wc == 0)) {
+          floatx16 tq;
+          zero(tq);
 #pragma unroll
-    for (int t = 0; t < kSlots; ++t) {
-      if (t >= nt_i) continue;
-      const bf16* dyt = dYs + t * XT;
-      if (!(t == 0 && wr == 1 && wc == 0)) {
-        floatx16 tq;
-        zero(tq);
+          for (int kk = 0; kk < PP / 16; ++kk) {
+            const bf16x8 av = tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh);
+            const bf16x8 bv = tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh);
+            mfma(dS[t], av, bv);
+            mfma(tq, av, bv);
+          }
+          // G over the quadrant: lane l holds column l, registers the s rows (S^T read back
+          // from LDS in that layout, four rows per transposed read)
+          float rs = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < PP / 16; ++kk) {
-          const bf16x8 av = tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh);
-          const bf16x8 bv = tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh);
-          mfma(dS[t], av, bv);
-          mfma(tq, av, bv);
+          for (int r = 0; r < 4; ++r) {
+            const bf16x4 sv = ttr4<64>(St + t * SQ, 32 * wr + 8 * r + 4 * hh, 32 * wc + 16 * ((lane >> 4) & 1), lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rs = fmaf((float)sv[e], tq[4 * r + e], rs);
+          }
+          rs = add_xor32(rs);
+          if (hh == 0) red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
+        } else if (hh == 0) {
+          red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
         }
-        // G over the quadrant: lane l holds column l, registers the s rows; row sums per
-        // lane, column sums per register (both from the same products, so that the
-        // chunk total of rowG - colG cancels as the reference's does)
-        float rs = 0.0f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float gv = (float)S[t][v >> 3][v & 7] * tq[v];
-          rs += gv;
-          colacc[v] += gv;
-        }
-        rs += __shfl_xor(rs, 32, 64);
-        if (hh == 0) red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
-      } else if (hh == 0) {
-        red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
       }
-      if (pt < PT) {
+    } else if (pt >= PT) {
+      // dX waves past the p tiles add zeros
+      if (hh == 0) {
+        red_e[pt * 64 + 32 * sr + l32] = 0.0f;
+        red_x[pt * 64 + 32 * sr + l32] = 0.0f;
+        red_col[pt * 64 + 32 * sr + l32] = 0.0f;
+      }
+      if (lane == 0) red_d[w - 4] = 0.0f;
+    } else {
+      // ---- dX^T += dY'^T S over the tiles (i, j); state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
+      floatx16 dXa, dXs;
+      zero(dXa);
+      zero(dXs);
+#pragma unroll
+      for (int t = 0; t < kSlots; ++t) {
+        if (t >= nt_i) continue;
+        const bf16* dyt = dYs + t * XT;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
           mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh));
       }
-    }
-    // ---- colG_s over this wave's l: sum over the lanes of each register ----
-    {
-      const float cg = half_reduce16(colacc, lane);
-      const int idx = (lane >> 1) & 15;
-      if ((lane & 1) == 0) red_col[wc * 64 + 32 * wr + 8 * (idx >> 2) + 4 * hh + (idx & 3)] = cg;
-    }
-    // ---- state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
-    floatx16 dXs;
-    zero(dXs);
-    if (pt < PT) {
 #pragma unroll
       for (int kk = 0; kk < NP / 16; ++kk)
         mfma(dXs, tld8<NP>(dstT, 32 * pt + l32, 16 * kk + 8 * hh), tld8<NP>(Bt, 32 * sr + l32, 16 * kk + 8 * hh));
-    }
 
-    // ---- per token s (lane) of block j: scale, sums, dx (waves past the p tiles add zeros) ----
-    if (pt >= PT) {
-      if (hh == 0) {
-        red_e[pt * 64 + 32 * sr + l32] = 0.0f;
-        red_x[pt * 64 + 32 * sr + l32] = 0.0f;
-      }
-      if (lane == 0) red_d[w] = 0.0f;
-    } else {
+      // ---- per token s (lane) of block j: scale, sums, dx ----
       const int s_loc = 32 * sr + l32, sg = 64 * j + s_loc;
-      const float c2 = s_cs2[sg], cj2 = s_cs2[64 * j + 63], cl2 = s_cs2[Qpad - 1];
-      const float gs = exp2_fast(cj2 - c2);
-      const float dw = cl2 - c2;
+      const float gs = exp2_fast(e_cj2 - e_c2);
+      const float dw = e_cl2 - e_c2;
       const float ws = sg < ci.len ? exp2_fast(clamp_med3(dw, -SSD_T2, SSD_T2)) : 0.0f;
       const float pw = fabsf(dw) < SSD_T2 ? 1.0f : 0.0f;
-      const float dts = s_dt[sg];
-      float esum = 0.0f, xsum = 0.0f, dsum = 0.0f;
+      const float dts = e_dt;
+      float esum = 0.0f, xsum = 0.0f, dsum = 0.0f, csum = 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int p0 = 32 * pt + 8 * r + 4 * hh;
         const bf16x4 xv = tld4<PP>(xu, s_loc, p0);
         const bf16x4 yv = tld4<PP>(dyu, s_loc, p0);
+        const bf16x4 sv = tld4<PP>(xs, s_loc, p0);
         bf16x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -355,6 +365,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           const float xf = (float)xv[e], yf = (float)yv[e];
           const float di = gs * dXa[v], ds = ws * dXs[v];
           const float dX = di + ds;
+          csum = fmaf((float)sv[e], dXa[v], csum);
           esum = fmaf(xf, ds, esum);
           xsum = fmaf(xf, dX, xsum);
           dsum = fmaf(xf, yf, dsum);
@@ -362,21 +373,23 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         }
         *reinterpret_cast<bf16x4*>(ot + toff<PP>(s_loc, p0)) = o;
       }
-      esum += __shfl_xor(esum, 32, 64);
-      xsum += __shfl_xor(xsum, 32, 64);
-      for (int o2 = 32; o2 > 0; o2 >>= 1) dsum += __shfl_xor(dsum, o2, 64);
+      esum = add_xor32(esum);
+      xsum = add_xor32(xsum);
+      csum = add_xor32(csum);
+      dsum = wave_sum(dsum);
       if (hh == 0) {
         red_e[pt * 64 + s_loc] = esum * dts * pw;
         red_x[pt * 64 + s_loc] = xsum;
+        red_col[pt * 64 + s_loc] = csum;
       }
-      if (lane == 0) red_d[w] = dsum;
+      if (lane == 0) red_d[w - 4] = dsum;
     }
-    if (h + 1 < h_hi) put_scales();
   }
   __syncthreads();
   flush(h_hi - 1);
 
   // ---- dS tiles, summed over the slice's heads (zero outside the causal mask) ----
+  if (xrole) return;
   float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
 #pragma unroll
   for (int t = 0; t < kSlots; ++t) {
@@ -416,7 +429,7 @@ static hipError_t bwd_fact_t(const SsdDims& d, const BwdFactArgs& a, hipStream_t
   const int blocks = (U + 7) / 8 * 8 * (d.Qpad / 64);
   const size_t lds = BwdFactLds<PT, NT>::bytes(d.Qpad);
   ensure_lds(k_bwd_fact<PT, NT>, lds);
-  hipLaunchKernelGGL((k_bwd_fact<PT, NT>), dim3(blocks), dim3(256), lds, s, d, a);
+  hipLaunchKernelGGL((k_bwd_fact<PT, NT>), dim3(blocks), dim3(kThreads), lds, s, d, a);
   return hipGetLastError();
 }
 

@@ -250,6 +250,25 @@ __device__ __forceinline__ float clamp_med3(float v, float lo, float hi) { retur
 #define SSD_LOG2E 1.4426950408889634f
 #define SSD_T2 (20.0f * SSD_LOG2E)
 
+// v + v of lane L ^ 32, with no LDS round trip: v_permlane32_swap of v with
+// itself yields the lower half-wave's values in one result and the upper
+// half's in the other, for every lane. Both lanes of a pair get the same sum.
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of v over the wave, in every lane: DPP within each 16-lane row, then
+// v_permlane16_swap / v_permlane32_swap across rows.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));  // row_mirror
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return add_xor32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
 // Sum of v over the 32 lanes of each half-wave, for 16 values at once.
 // Afterwards lane L returns the sum of v[(L >> 1) & 15] over its half.
 __device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
