@@ -13,7 +13,9 @@
 // Each head's inputs (h_in, dst, the block's x and dy rows, cs, dt) are moved
 // into LDS by buffer_load ... lds, two heads ahead through a ring of three
 // slots, so no register holds staged data and the loads of two heads are in
-// flight while one computes. LDS rows are unpadded; 16-byte granules are
+// flight while one computes. The ring allows one block per CU, so its 8 waves
+// take two roles that share each SIMD and overlap: waves 0-3 build dC and the
+// decay gradient (and issue the ring loads), waves 4-7 build dB. LDS rows are unpadded; 16-byte granules are
 // permuted per row so that transposed reads (h_in, dst) and row reads (x, dy)
 // hit distinct banks.
 #include "ssd_launch.h"
@@ -62,7 +64,7 @@ struct GemmCfg {
   // bytes of one ring slot: h_in, dst, x, dy, then cs, dt, cs_last, spare (64 floats each)
   static constexpr size_t kSlot = (size_t)(2 * HIN + 2 * XT) * 2 + 4 * 256;
   static constexpr size_t bytes = 3 * kSlot;
-  // DMA instructions per wave and head (4 waves)
+  // DMA instructions per issuing wave and head (waves 0-3)
   static constexpr int kTileDma = HIN / 512;    // 1 KB per instruction
   static constexpr int kRowDma = XT / 512;
   static constexpr int kPerWave = (2 * kTileDma + 2 * kRowDma) / 4 + 1;
@@ -78,7 +80,7 @@ __device__ __forceinline__ void wait_vm() {
 }  // namespace
 
 template <int PT, int NT>
-__global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                   const float* __restrict__ cs, const float* __restrict__ dt,
                                                   const bf16* __restrict__ x, const bf16* __restrict__ dy,
                                                   const bf16* __restrict__ hin, const bf16* __restrict__ dst,
@@ -101,7 +103,8 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const ChunkInfo ci = chunks[c];
   if (64 * kb >= ci.len) return;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int th = w & 1, nh = w >> 1;
+  const bool brole = w >= 4;  // dB waves (else dC waves, which also issue the ring loads)
+  const int th = w & 1, nh = (w >> 1) & 1;
   int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
   const int t_loc = 32 * th + l32;         // token of this lane within block kb
   const int t = 64 * kb + t_loc;           // ... within the chunk
@@ -164,12 +167,10 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)sc, 4, off, 0, 0, 0);
   };
 
-  floatx16 aC[NTW], aB[NTW];
+  // dC (waves 0-3) or dB (waves 4-7) rows t, columns n of the wave's n tiles
+  floatx16 acc[NTW];
 #pragma unroll
-  for (int q = 0; q < NTW; ++q) {
-    zero(aC[q]);
-    zero(aB[q]);
-  }
+  for (int q = 0; q < NTW; ++q) zero(acc[q]);
   // C[t][n] at this lane's accumulator rows n (the Y_off part of the decay gradient)
   const __amdgpu_buffer_rsrc_t rC = buf_rsrc(Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
   bf16x4 Cv[NTW][4];
@@ -179,20 +180,24 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n0 = 32 * nt + 8 * r + 4 * hh;
-      const bool ok = tok && nt < NT && n0 < d.N;
+      const bool ok = !brole && tok && nt < NT && n0 < d.N;
       Cv[q][r] = __builtin_bit_cast(
           bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rC, ok ? (int)(t * brow + n0) * 2 : SSD_BUF_SIZE, 0, 0));
     }
   }
 
-  issue(h0, 0);
-  if (h0 + 1 < h1) issue(h0 + 1, 1);
+  if (!brole) {
+    issue(h0, 0);
+    if (h0 + 1 < h1) issue(h0 + 1, 1);
+  }
   for (int h = h0; h < h1; ++h) {
     // this wave's loads of head h are done (those of h + 1 may still fly); then every wave's
-    if (h + 1 < h1) wait_vm<Cfg::kPerWave>();
-    else wait_vm<0>();
+    if (!brole) {
+      if (h + 1 < h1) wait_vm<Cfg::kPerWave>();
+      else wait_vm<0>();
+    }
     __syncthreads();  // head h visible in LDS; slot (h + 2) % 3 is free (head h - 1 done)
-    if (h + 2 < h1) issue(h + 2, (h + 2 - h0) % 3);
+    if (!brole && h + 2 < h1) issue(h + 2, (h + 2 - h0) % 3);
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
@@ -206,37 +211,36 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     const float dtt = d.has_dt ? scal[64 + t_loc] : 1.0f;
     const float et = exp_clamp(cst), pt_ = clamp_pass(cst);
     const float wdt = exp_clamp(csl - cst) * dtt;
-    bf16x8 yf[NK], xf[NK];
+    // dC waves: T = h_in dy_t^T (per n tile), dC += exp(clamp(cs_t)) T, decay term C_t . T;
+    // dB waves: U = dst x_t^T, dB += w_t dt_t U
+    const bf16* tile = brole ? td_ : th_;
+    const bf16* rows = brole ? tx : ty;
+    const float sc = brole ? wdt : et;
+    bf16x8 rf[NK];
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
-      yf[kk] = swz_nat8<PP>(ty, t_loc, 16 * kk + 8 * hh);
-      xf[kk] = swz_nat8<PP>(tx, t_loc, 16 * kk + 8 * hh);
-    }
+    for (int kk = 0; kk < NK; ++kk) rf[kk] = swz_nat8<PP>(rows, t_loc, 16 * kk + 8 * hh);
     float osum = 0.0f;
 #pragma unroll
     for (int q = 0; q < NTW; ++q) {
       const int nt = nh * NTW + q;
       if (nt >= NT) continue;
-      floatx16 T, U;
+      floatx16 T;
       zero(T);
-      zero(U);
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        mfma(T, swz_tr8<NP>(th_, 16 * kk, 32 * nt, lane), yf[kk]);
-        mfma(U, swz_tr8<NP>(td_, 16 * kk, 32 * nt, lane), xf[kk]);
+      for (int kk = 0; kk < NK; ++kk) mfma(T, swz_tr8<NP>(tile, 16 * kk, 32 * nt, lane), rf[kk]);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[q][v] = fmaf(sc, T[v], acc[q][v]);
+      if (!brole) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) osum += (float)Cv[q][r][e] * T[4 * r + e];
       }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        aC[q][v] = fmaf(et, T[v], aC[q][v]);
-        aB[q][v] = fmaf(wdt, U[v], aB[q][v]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) osum += (float)Cv[q][r][e] * T[4 * r + e];
     }
-    osum += __shfl_xor(osum, 32, 64);
-    if (hh == 0 && tok) dcs_off[((int64_t)nh * MC * d.H + (int64_t)c * d.H + h) * Qpad + t] = osum * et * pt_;
+    if (!brole) {
+      osum = add_xor32(osum);
+      if (hh == 0 && tok) dcs_off[((int64_t)nh * MC * d.H + (int64_t)c * d.H + h) * Qpad + t] = osum * et * pt_;
+    }
   }
 
   // ---- tile terms: dC += dS[kb, j] B_j (j <= kb), dB += dS[i, kb]^T C_i (i >= kb) ----
@@ -250,7 +254,7 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   // heads of the group the factorised kernel left to the exact fixup: their dS is in dS_fix
   bool slow = false;
   if (fast)
-    for (int hq = h0 + (int)threadIdx.x; hq < h1; hq += 256) slow = slow || fast[(int64_t)c * d.H + hq] == 0;
+    for (int hq = h0 + (int)threadIdx.x; hq < h1; hq += 512) slow = slow || fast[(int64_t)c * d.H + hq] == 0;
   const bool any_fix = __syncthreads_or(slow);
   const float* dSf = dS_fix + ((int64_t)c * d.G + g) * nb * nb * 4096;
   for (int pass = 0; pass < 2; ++pass) {
@@ -259,7 +263,7 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       __syncthreads();
       const int ti = pass == 0 ? kb : m, tj = pass == 0 ? m : kb;
       const float* src = dSc + (ti * nb + tj) * 4096;
-      for (int id = threadIdx.x; id < 512; id += 256) {
+      for (int id = threadIdx.x; id < 512; id += 512) {
         const int r = id >> 3, k = (id & 7) * 8;
         floatx4 s0 = *reinterpret_cast<const floatx4*>(src + r * 64 + k);
         floatx4 s1 = *reinterpret_cast<const floatx4*>(src + r * 64 + k + 4);
@@ -278,14 +282,15 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
         *reinterpret_cast<bf16x8*>(tS + toff<64, tpitch<64>()>(r, k)) = v;
       }
       {
-        TileStage<64, NP, 256> st;
+        TileStage<64, NP, 512> st;
         tstage_load_v(st, (pass == 0 ? Bm : Cm) + (int64_t)(ci.row0 + 64 * m) * brow + (int64_t)g * d.N, brow,
                       min(64, ci.len - 64 * m), d.N);
-        tstage_store<64, NP, 256, PI>(st, tBC);
+        tstage_store<64, NP, 512, PI>(st, tBC);
       }
       __syncthreads();
       lane = opaque_lane();
       hh = lane >> 5;
+      if (brole != (pass == 1)) continue;  // pass 0 is the dC waves', pass 1 the dB waves'
 #pragma unroll
       for (int q = 0; q < NTW; ++q) {
         const int nt = nh * NTW + q;
@@ -295,9 +300,9 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
           const bf16x8 av = ttr_std<NP, PI>(tBC, kk, 32 * nt, lane);
           // pass 0: B[k = s][j = t] = dS[t][s] (row t, natural); pass 1: B[k = l][j = t] (transposed)
           if (pass == 0)
-            mfma(aC[q], av, tld8<64, tpitch<64>()>(tS, t_loc, kk + 8 * hh));
+            mfma(acc[q], av, tld8<64, tpitch<64>()>(tS, t_loc, kk + 8 * hh));
           else
-            mfma(aB[q], av, ttr_std<64, tpitch<64>()>(tS, kk, 32 * th, lane));
+            mfma(acc[q], av, ttr_std<64, tpitch<64>()>(tS, kk, 32 * th, lane));
         }
       }
     }
@@ -312,14 +317,10 @@ __global__ void __launch_bounds__(256) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       for (int r = 0; r < 4; ++r) {
         const int n0 = 32 * nt + 8 * r + 4 * hh;
         if (n0 >= d.N) continue;
-        bf16x4 oc, ob;
+        bf16x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          oc[e] = (bf16)aC[q][4 * r + e];
-          ob[e] = (bf16)aB[q][4 * r + e];
-        }
-        *reinterpret_cast<bf16x4*>(dC + row + n0) = oc;
-        *reinterpret_cast<bf16x4*>(dB + row + n0) = ob;
+        for (int e = 0; e < 4; ++e) o[e] = (bf16)acc[q][4 * r + e];
+        *reinterpret_cast<bf16x4*>((brole ? dB : dC) + row + n0) = o;
       }
     }
   }
@@ -344,7 +345,7 @@ static hipError_t bwd_gemm_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in
                              hipStream_t s) {
   ensure_lds(k_bwd_gemm<PT, NT>, GemmCfg<PT, NT>::bytes);
   const int nbq = d.Qpad / 64;
-  hipLaunchKernelGGL((k_bwd_gemm<PT, NT>), dim3((d.max_chunks + 7) / 8 * 8 * nbq, d.G), dim3(256), (GemmCfg<PT, NT>::bytes), s,
+  hipLaunchKernelGGL((k_bwd_gemm<PT, NT>), dim3((d.max_chunks + 7) / 8 * 8 * nbq, d.G), dim3(512), (GemmCfg<PT, NT>::bytes), s,
                      d, b.chunks, b.cs, in.dt, reinterpret_cast<const bf16*>(in.x),
                      reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(b.hin), b.dst16,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), b.dS_tiles,
