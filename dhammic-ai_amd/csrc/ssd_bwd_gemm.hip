@@ -23,39 +23,6 @@
 
 namespace {
 
-// Permuted granule of logical granule g in row r of a W-wide bf16 tile.
-// Tiles read with ds_read_b64_tr_b16 (four rows, two granules per 16 lanes):
-template <int W>
-__device__ __forceinline__ int swz_tr(int r, int g) {
-  return W >= 64 ? g ^ ((r & 3) << 1) : g;
-}
-// Tiles read by rows (16 consecutive rows at one granule):
-template <int W>
-__device__ __forceinline__ int swz_nat(int r, int g) {
-  return W == 128 ? g ^ (r & 15) : (W == 64 ? g ^ ((r >> 1) & 7) : g ^ ((r >> 2) & 3));
-}
-
-// k-contiguous operand with i = mbase + L % 32 from a transposed-read tile
-// (row index k), as ttr_std does for padded tiles.
-template <int W>
-__device__ __forceinline__ bf16x4 swz_tr4(const bf16* t, int kb, int m0, int L) {
-  const int q = L & 15;
-  const int r = kb + (q >> 2), col = m0 + ((q & 3) << 2);
-  const bf16* p = t + r * W + (swz_tr<W>(r, col >> 3) << 3) + (col & 7);
-  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
-  return __builtin_bit_cast(bf16x4, v);
-}
-template <int W>
-__device__ __forceinline__ bf16x8 swz_tr8(const bf16* t, int k0, int mbase, int L) {
-  const int h = L >> 5;
-  const int m0 = mbase + (((L >> 4) & 1) << 4);
-  return cat8(swz_tr4<W>(t, k0 + 8 * h, m0, L), swz_tr4<W>(t, k0 + 8 * h + 4, m0, L));
-}
-template <int W>
-__device__ __forceinline__ bf16x8 swz_nat8(const bf16* t, int r, int col) {
-  return *reinterpret_cast<const bf16x8*>(t + r * W + (swz_nat<W>(r, col >> 3) << 3));
-}
-
 template <int PT, int NT>
 struct GemmCfg {
   static constexpr int PP = 32 * PT, NP = 32 * NT;
@@ -70,12 +37,6 @@ struct GemmCfg {
   static constexpr int kPerWave = (2 * kTileDma + 2 * kRowDma) / 4 + 1;
   static_assert((2 * kTileDma + 2 * kRowDma) % 4 == 0, "DMA split");
 };
-
-// vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt 7, lgkmcnt 15)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  __builtin_amdgcn_s_waitcnt(0xF70 | (N & 15) | ((N >> 4) << 14));
-}
 
 }  // namespace
 

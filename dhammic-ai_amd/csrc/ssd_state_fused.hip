@@ -12,95 +12,285 @@
 // and dinit = run. The running state stays in the MFMA accumulator registers;
 // nothing but hin / dst (bf16) and the final / initial state is written.
 //
-// One block per (32-wide n tile, head, sequence) with one wave per 32-wide p
-// tile (64 * Ppad / 32 threads); wave w owns the 32 x 32 state tile (p tile w,
-// the block's n tile). Blocks of one (head, sequence) are numbered onto one XCD
-// (same block index mod 8) so their shared x / dy rows are read from HBM once.
-// Tokens are staged 64 at a time (x or dy rows, B or C columns scaled per
-// token) and both MFMA operands are read with ds_read_b64_tr_b16 (the
-// contraction is over tokens, the tiles' row index; the tiles use the
-// transpose-read pitch). Global loads run three 64-token steps ahead through a
-// ring of three register stages.
+// One block per (pair of 32-wide n tiles, head, sequence) with one wave per
+// (32-wide p tile, n tile of the pair); wave w owns the 32 x 32 state tile
+// (p tile w % PT, n tile w / PT). Blocks of one (head, sequence) are numbered
+// onto one XCD (same block index mod 8) so their shared x / dy rows come from
+// HBM once. Tokens go 64 at a time through a ring of three LDS slots filled by
+// buffer_load ... lds (x or dy rows, the pair's B or C columns, cs and dt),
+// issued two steps ahead with explicit vmcnt waits, so no register holds
+// staged data and every step's wait counts exactly. Both MFMA operands are
+// read with ds_read_b64_tr_b16 from granule-permuted rows (the contraction is
+// over tokens, the tiles' row index); the per-token factor is applied to the
+// B / C operand in registers after the read.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
 
+namespace {
+
 template <int PT>
-struct StateStage {
-  static constexpr int NTHR = 64 * PT;
-  TileStage<64, 32 * PT, NTHR> u;  // x or dy rows, all Ppad columns
-  TileStage<64, 32, NTHR> v;       // B or C rows, the block's 32 columns
+struct StateCfg {
+  static constexpr int PP = 32 * PT;            // state rows per block
+  static constexpr int NW = 2 * PT;             // waves: (p tile, n tile of the pair)
+  static constexpr int NTHR = 64 * NW;
+  static constexpr int R = 3;                   // ring slots
+  static constexpr int UB = 64 * PP * 2;        // x / dy rows of a step
+  static constexpr int VB = 64 * 64 * 2;        // B / C rows of a step, the pair's 64 columns
+  static constexpr int SLOT = UB + VB + NW * 256;  // + one 64-float row per wave (cs, dt, spare)
+  static constexpr int UI = UB / 1024, VI = VB / 1024;  // 1 KB DMA instructions
+  static constexpr int PERW = (UI + VI) / NW;   // row DMAs per wave and step
+  static constexpr int D = PERW + 1;            // DMAs per wave and step (+ one scalar row)
+  static_assert((UI + VI) % NW == 0, "DMA split");
+  static constexpr int TP = 40;                 // s_tile row pitch (elements)
+  static size_t bytes(bool bwd) {
+    return (size_t)R * SLOT + NW * 64 * 4 + NW * 32 * TP * 2 + (bwd ? NW * 2048 : 0) + 64;
+  }
 };
 
-template <int PT>
-__device__ __forceinline__ void state_load(StateStage<PT>& st, const bf16* U, const bf16* V, int64_t urow,
-                                           int64_t vrow, int64_t row0, int t0, int len, int P, int nw,
-                                           int64_t ucol, int64_t vcol) {
-  const int nrows = min(64, len - t0);
-  tstage_load_v(st.u, U + (row0 + t0) * urow + ucol, urow, nrows, P);
-  tstage_load_v(st.v, V + (row0 + t0) * vrow + vcol, vrow, nrows, nw);
+}  // namespace
+
+// Everything a step needs besides LDS (wave-uniform unless noted).
+struct StateCtx {
+  SsdDims d;
+  const ChunkInfo* chunks;
+  const float* cs;
+  const float* dt;
+  const bf16* U;
+  const bf16* V;
+  bf16* hst;
+  const bf16* hin_in;
+  float* dtot_part;
+  int64_t urow, vrow, ucol, vcol;
+  int h, np, w, pt, ntl, nt, NTn, c0, c1, nch;
+  bool nt_ok;
+};
+
+// A walk position: chunk index k of the sequence, token offset t in it, and the
+// chunk's table entry (fetched when the position enters the chunk, a step before use).
+struct Cursor {
+  int k, t, c;
+  ChunkInfo ci;
+};
+
+template <bool FWD>
+__device__ __forceinline__ void cursor_fetch(const StateCtx& x, Cursor& u) {
+  const int kc = min(u.k, x.nch - 1);
+  u.c = __builtin_amdgcn_readfirstlane(FWD ? x.c0 + kc : x.c1 - 1 - kc);
+  u.ci = x.chunks[u.c];
 }
 
-// Stores the staged rows; V rows are scaled by coef[r] (fp32) before rounding.
-template <int PT>
-__device__ __forceinline__ void state_store(const StateStage<PT>& st, bf16* tu, bf16* tv, const float* coef) {
-  constexpr int NTHR = StateStage<PT>::NTHR;
-  tstage_store<64, 32 * PT, NTHR, tpitch_tr<32 * PT>()>(st.u, tu);
+// One step's DMAs into ring slot `nxt`: StateCfg::D per wave, also past the last step
+// (then masked to zeros), so that every step issues the same count. Advances the
+// issue cursor.
+template <int PT, bool FWD>
+__device__ __forceinline__ void state_issue(const StateCtx& x, unsigned char* __restrict__ nxt, Cursor& u, int lane) {
+  using Cfg = StateCfg<PT>;
+  constexpr int PP = Cfg::PP;
+  const SsdDims& d = x.d;
+  const bool live = u.k < x.nch;
+  const int c = u.c;
+  const ChunkInfo ci = u.ci;
+  const int t0i = live ? u.t : 0;
+  const int nrows = live ? min(64, ci.len - t0i) : 0;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(x.U + (int64_t)(ci.row0 + t0i) * x.urow + x.ucol);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(x.V + (int64_t)(ci.row0 + t0i) * x.vrow + x.vcol);
+  constexpr int UG = PP / 8, URI = 64 / UG;  // granules per U row, U rows per DMA
 #pragma unroll
-  for (int q = 0; q < TileStage<64, 32, NTHR>::PER; ++q) {
-    const int id = threadIdx.x + q * NTHR;
-    if (TileStage<64, 32, NTHR>::NVEC % NTHR == 0 || id < TileStage<64, 32, NTHR>::NVEC) {
-      const int r = id / 4, k = (id % 4) * 8;
-      const float sc = coef[r];
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)st.v.v[q][e] * sc);
-      *reinterpret_cast<bf16x8*>(tv + toff<32, tpitch_tr<32>()>(r, k)) = o;
+  for (int q = 0; q < Cfg::PERW; ++q) {
+    const int qq = x.w * Cfg::PERW + q;
+    if (qq < Cfg::UI) {
+      const int r = qq * URI + lane / UG, j = lane % UG;
+      const int gcol = swz_tr<PP>(r, j) << 3;
+      const bool ok = r < nrows && gcol < d.P;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ru, (__attribute__((address_space(3))) void*)(nxt + qq * 1024), 16,
+                                               ok ? (int)((r * x.urow + gcol) * 2) : SSD_BUF_SIZE, 0, 0, 0);
+    } else {
+      const int vi = qq - Cfg::UI;
+      const int r = vi * 8 + lane / 8, j = lane % 8;
+      const int gcol = swz_tr<64>(r, j) << 3;
+      const bool ok = r < nrows && 64 * x.np + gcol < d.N;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv,
+                                               (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + vi * 1024),
+                                               16, ok ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE, 0, 0, 0);
+    }
+  }
+  // scalar rows: wave 0 cs of the step's tokens, wave 1 dt (forward), the others nothing
+  {
+    const float* csh = x.cs + ((int64_t)c * d.H + x.h) * d.Qpad;
+    const bool dtw = FWD && d.has_dt && x.w == 1;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(dtw ? x.dt + (int64_t)(ci.row0 + t0i) * d.H + x.h : csh);
+    const int off = x.w == 0 ? (t0i + lane) * 4 : (dtw && lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB + x.w * 256), 4, off, 0, 0, 0);
+  }
+  if (live) {
+    u.t += 64;
+    if (u.t >= ci.len) {
+      ++u.k;
+      u.t = 0;
+      cursor_fetch<FWD>(x, u);
     }
   }
 }
 
-// Scalars of one 64-token step: its chunk's row range and total log-decay, and
-// the per-token inputs of the coefficients (threads < 64: token t0 + tid).
-struct StepCoef {
-  float cs_tok, dt_tok, tot;
-  int row0, len;
-};
+// One 64-token step: refill slot `nxt`, consume slot `cur`. Every LDS access of the
+// step goes through these distinct __restrict__ pointers, which tells the compiler
+// that the new DMAs do not write what the step reads: it then adds no wait of its
+// own for them, and the slot waits stay the explicit ones of the caller.
+template <int PT, bool FWD>
+__device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
+                                           unsigned char* __restrict__ nxt, float* __restrict__ cw,
+                                           bf16* __restrict__ tw, bf16* __restrict__ hbw, float* __restrict__ red,
+                                           Cursor& ui, Cursor& uc, float& tot, int& st, int& s_start,
+                                           floatx16& acc, floatx16& run) {
+  using Cfg = StateCfg<PT>;
+  constexpr int PP = Cfg::PP, TP = Cfg::TP;
+  const SsdDims& d = x.d;
+  const int lane = opaque_lane();
+  state_issue<PT, FWD>(x, nxt, ui, lane);
+  const int c = uc.c;
+  const int clen = uc.ci.len;
+  int& t0 = uc.t;
+  const int64_t soff = ((int64_t)c * d.H + x.h) * d.Ppad * d.Npad;
+  const int prow0 = 32 * x.pt;
+  if (t0 == 0) {
+    s_start = st;
+    // state entering (forward) / gradient leaving (backward) chunk c: accumulator layout
+    // -> this wave's LDS tile -> 16-byte row pieces (16 rows x 64 bytes per store)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) tw[acc_row(v, lane) * TP + (lane & 31)] = (bf16)run[v];
+    __builtin_amdgcn_wave_barrier();
+    if (x.nt_ok) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
+        const int64_t o = soff + (int64_t)(prow0 + r) * d.Npad + 32 * x.nt + c8;
+        *reinterpret_cast<bf16x8*>(x.hst + o) = *reinterpret_cast<const bf16x8*>(tw + r * TP + c8);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (!FWD) {
+      // this wave's 32 x 32 tile of h_in[c], consumed at the end of the chunk
+      const __amdgpu_buffer_rsrc_t rh = buf_rsrc(x.hin_in + soff);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int r = 16 * q + lane / 4, c8 = (lane % 4) * 8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rh, (__attribute__((address_space(3))) void*)(hbw + q * 512), 16,
+            x.nt_ok ? (int)(((prow0 + r) * d.Npad + 32 * x.nt + c8) * 2) : SSD_BUF_SIZE, 0, 0, 0);
+      }
+    }
+  }
+  const bf16* tu = reinterpret_cast<const bf16*>(cur);
+  const bf16* tv = reinterpret_cast<const bf16*>(cur + Cfg::UB);
+  const float* scal = reinterpret_cast<const float*>(cur + Cfg::UB + Cfg::VB);
+  // per-token factor of the step's B / C rows (lane = token), for this wave's own use
+  {
+    const float cst = scal[lane];
+    const float dtt = (FWD && d.has_dt) ? scal[64 + lane] : 1.0f;
+    const float f = FWD ? exp_clamp(tot - cst) * dtt : exp_clamp(cst);
+    cw[lane] = t0 + lane < clen ? f : 0.0f;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 64; kk += 16) {
+    const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5));
+    const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5) + 4);
+    bf16x8 b = swz_tr8<64>(tv, kk, 32 * x.ntl, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b[e] = (bf16)((float)b[e] * f0[e]);
+      b[4 + e] = (bf16)((float)b[4 + e] * f1[e]);
+    }
+    mfma(acc, swz_tr8<PP>(tu, kk, prow0, lane), b);
+  }
+  t0 += 64;
+  ++st;
+  if (t0 >= clen) {
+    // end of chunk c
+    const float dec = exp_clamp(tot);
+    if (!FWD) {
+      // the h_in tile's DMAs were issued at the chunk's first step, before the ring DMAs
+      // of the (st - 1 - s_start) steps since
+      switch (st - 1 - s_start) {
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<Cfg::D>(); break;
+        case 2: wait_vm<2 * Cfg::D>(); break;
+        default: wait_vm<3 * Cfg::D>(); break;
+      }
+      float contrib = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hbw[acc_row(v, lane) * 32 + (lane & 31)];
+      contrib *= dec * clamp_pass(tot);
+      contrib = wave_sum(contrib);
+      if (lane == 0) red[x.w] = contrib;
+      lds_barrier();
+      if (x.nt_ok && x.pt == 0 && lane == 0) {
+        float sum = 0.0f;
+        for (int q = 0; q < PT; ++q) sum += red[x.ntl * PT + q];
+        x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn + x.nt] = sum;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) run[v] = dec * run[v] + acc[v];
+    zero(acc);
+    ++uc.k;
+    t0 = 0;
+    // the next chunk's entry and total log-decay, a step ahead of their use
+    cursor_fetch<FWD>(x, uc);
+    tot = x.cs[((int64_t)uc.c * d.H + x.h) * d.Qpad + d.Qpad - 1];
+  }
+}
 
 template <int PT, bool FWD>
-__global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2, 2))) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
                                                          const float* __restrict__ cs, const float* __restrict__ dt,
                                                          const bf16* __restrict__ U, const bf16* __restrict__ V,
                                                          bf16* __restrict__ hst, const bf16* __restrict__ hin_in,
                                                          const void* __restrict__ s_in, void* __restrict__ s_out,
                                                          int state_bf16, float* __restrict__ dtot_part) {
-  constexpr int PP = 32 * PT;
-  constexpr int UPI = tpitch_tr<PP>(), VPI = tpitch_tr<32>();
-  __shared__ __align__(16) bf16 tu[2][tsize<64, PP, UPI>()];
-  __shared__ __align__(16) bf16 tv[2][tsize<64, 32, VPI>()];
-  __shared__ float coef[2][64];
-  __shared__ float red[4];
-  // per-wave 32 x 32 bf16 tile between the accumulator layout and whole 64-byte row
-  // pieces of HBM: the state written at a chunk start, and (backward) h_in at its end
-  constexpr int TP = 40;  // row pitch (elements)
-  __shared__ __align__(16) bf16 s_tile[PT][32 * TP];
-  // block -> (n tile, unit = (head, sequence)); the n tiles of a unit share an XCD
-  const int NTn = d.Npad / 32;
-  const int x8 = blockIdx.x & 7, rr = blockIdx.x >> 3;
-  const int nt = rr % NTn;
-  const int unit = (rr / NTn) * 8 + x8;
-  if (unit >= d.H * d.nseq) return;
-  const int h = unit % d.H, sq = unit / d.H;
-  const int g = h / d.hpg;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int64_t urow = (int64_t)d.H * d.P, vrow = (int64_t)d.G * d.N;
-  const int64_t ucol = (int64_t)h * d.P, vcol = (int64_t)g * d.N + 32 * nt;
-  const int nw = min(32, d.N - 32 * nt);  // valid columns of the block's n tile
-  const int n = 32 * nt + (lane & 31);
-  const int prow0 = 32 * w;
+  using Cfg = StateCfg<PT>;
+  constexpr int TP = Cfg::TP, SLOT = Cfg::SLOT;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* cw = reinterpret_cast<float*>(smem + Cfg::R * SLOT);             // [NW][64] per-token factors
+  bf16* s_tile = reinterpret_cast<bf16*>(cw + Cfg::NW * 64);              // [NW][32][TP]
+  bf16* hb = s_tile + Cfg::NW * 32 * TP;                                  // [NW][32][32] (backward: h_in)
+  float* red = reinterpret_cast<float*>(hb + (FWD ? 0 : Cfg::NW * 1024)); // [NW]
 
-  // running state: rows p = 32 w + acc_row(v), column n
+  // block -> (n tile pair, unit = (head, sequence)); the pairs of a unit share an XCD
+  StateCtx x;
+  x.d = d;
+  x.NTn = d.Npad / 32;
+  const int NPR = (x.NTn + 1) / 2;
+  const int x8 = blockIdx.x & 7, rr = blockIdx.x >> 3;
+  x.np = rr % NPR;
+  const int unit = (rr / NPR) * 8 + x8;
+  if (unit >= d.H * d.nseq) return;
+  x.h = unit % d.H;
+  const int sq = unit / d.H;
+  const int g = x.h / d.hpg;
+  x.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  x.pt = x.w % PT;
+  x.ntl = x.w / PT;
+  x.nt = 2 * x.np + x.ntl;
+  x.nt_ok = x.nt < x.NTn;
+  x.chunks = chunks;
+  x.cs = cs;
+  x.dt = dt;
+  x.U = U;
+  x.V = V;
+  x.hst = hst;
+  x.hin_in = hin_in;
+  x.dtot_part = dtot_part;
+  x.urow = (int64_t)d.H * d.P;
+  x.vrow = (int64_t)d.G * d.N;
+  x.ucol = (int64_t)x.h * d.P;
+  x.vcol = (int64_t)g * d.N + 64 * x.np;
+  const int lane = threadIdx.x & 63;
+  const int n = 32 * x.nt + (lane & 31);
+  const int prow0 = 32 * x.pt;
+
+  // running state: rows p = 32 pt + acc_row(v), column n
   floatx16 run;
   zero(run);
   if (s_in) {
@@ -108,133 +298,42 @@ __global__ void __launch_bounds__(64 * PT) __attribute__((amdgpu_waves_per_eu(2,
     for (int v = 0; v < 16; ++v) {
       const int p = prow0 + acc_row(v, lane);
       if (p < d.P && n < d.N) {
-        const int64_t o = (((int64_t)sq * d.H + h) * d.P + p) * d.N + n;
+        const int64_t o = (((int64_t)sq * d.H + x.h) * d.P + p) * d.N + n;
         run[v] = state_bf16 ? (float)reinterpret_cast<const bf16*>(s_in)[o] : reinterpret_cast<const float*>(s_in)[o];
       }
     }
   }
-  const int c0 = seq_chunk0[sq], c1 = seq_chunk0[sq + 1];
-  const int nch = c1 - c0;
-  auto chunk_of = [&](int k) { return FWD ? c0 + k : c1 - 1 - k; };
+  wait_vm<0>();  // the ring's waits below count the ring's DMAs only
+  x.c0 = seq_chunk0[sq];
+  x.c1 = seq_chunk0[sq + 1];
+  x.nch = x.c1 - x.c0;
 
-  // load cursor (kl, tl): the next step whose inputs are fetched
-  int kl = 0, tl = 0;
-  auto load_next = [&](StateStage<PT>& st, StepCoef& cf) {
-    if (kl >= nch) return;
-    const int c = chunk_of(kl);
-    const ChunkInfo ci = chunks[c];
-    state_load<PT>(st, U, V, urow, vrow, ci.row0, tl, ci.len, d.P, nw, ucol, vcol);
-    cf.row0 = ci.row0;
-    cf.len = ci.len;
-    cf.tot = cs[((int64_t)c * d.H + h) * d.Qpad + d.Qpad - 1];
-    cf.cs_tok = 0.0f;
-    cf.dt_tok = 1.0f;
-    if (threadIdx.x < 64) {
-      const int l = tl + threadIdx.x;
-      cf.cs_tok = cs[((int64_t)c * d.H + h) * d.Qpad + min(l, d.Qpad - 1)];
-      if (FWD && d.has_dt && l < ci.len) cf.dt_tok = dt[(int64_t)(ci.row0 + l) * d.H + h];
-    }
-    tl += 64;
-    if (tl >= ci.len) {
-      ++kl;
-      tl = 0;
-    }
-  };
-
-  // compute cursor (k, t0)
-  int k = 0, t0 = 0, buf = 0;
+  Cursor ui{0, 0, 0, {}}, uc{0, 0, 0, {}};  // issue and compute cursors
+  float tot = 0.0f;                          // total log-decay of the compute cursor's chunk
+  if (x.nch > 0) {  // (an empty sequence passes its state through)
+    cursor_fetch<FWD>(x, ui);
+    uc = ui;
+    tot = cs[((int64_t)uc.c * d.H + x.h) * d.Qpad + d.Qpad - 1];
+    state_issue<PT, FWD>(x, smem, ui, lane);
+    state_issue<PT, FWD>(x, smem + SLOT, ui, lane);
+  }
   floatx16 acc;
   zero(acc);
-  bf16x8 hin_v[2];  // this lane's two 8-element row pieces of h_in (rows (lane + 64 q) / 4)
-  // one 64-token step on the inputs in (st, cf); refills them with the step three ahead
-  auto step = [&](StateStage<PT>& st, StepCoef& cf) {
-    const int c = chunk_of(k);
-    const int clen = cf.len;
-    const float tot = cf.tot;
-    const int64_t soff = ((int64_t)c * d.H + h) * d.Ppad * d.Npad;
-    if (t0 == 0) {
-      // state entering (forward) / gradient leaving (backward) chunk c: accumulator layout
-      // -> this wave's LDS tile -> 16-byte row pieces (16 rows x 64 bytes per store)
-      bf16* tw = s_tile[w];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) tw[acc_row(v, lane) * TP + (lane & 31)] = (bf16)run[v];
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
-        const int64_t o = soff + (int64_t)(prow0 + r) * d.Npad + 32 * nt + c8;
-        *reinterpret_cast<bf16x8*>(hst + o) = *reinterpret_cast<const bf16x8*>(tw + r * TP + c8);
-        if (!FWD) hin_v[q] = *reinterpret_cast<const bf16x8*>(hin_in + o);  // consumed at the end of the chunk
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
-    if (threadIdx.x < 64) {
-      const int l = t0 + threadIdx.x;
-      float v = 0.0f;
-      if (l < clen) v = FWD ? exp_clamp(tot - cf.cs_tok) * cf.dt_tok : exp_clamp(cf.cs_tok);
-      coef[buf][threadIdx.x] = v;
-    }
-    __syncthreads();  // coef visible; this buffer's previous readers are done
-    state_store<PT>(st, tu[buf], tv[buf], coef[buf]);
-    __syncthreads();
-    load_next(st, cf);  // st / cf are free now: refill with the step three ahead
-#pragma unroll
-    for (int kk = 0; kk < 64; kk += 16)
-      mfma(acc, ttr_std<PP, UPI>(tu[buf], kk, prow0, lane), ttr_std<32, VPI>(tv[buf], kk, 0, lane));
-    buf ^= 1;
-    t0 += 64;
-    if (t0 >= clen) {
-      // end of chunk c
-      const float dec = exp_clamp(tot);
-      if (!FWD) {
-        bf16* th = s_tile[w];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
-          *reinterpret_cast<bf16x8*>(th + r * TP + c8) = hin_v[q];
-        }
-        __builtin_amdgcn_wave_barrier();
-        float contrib = 0.0f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) contrib += run[v] * (float)th[acc_row(v, lane) * TP + (lane & 31)];
-        __builtin_amdgcn_wave_barrier();
-        contrib *= dec * clamp_pass(tot);
-        for (int o = 32; o > 0; o >>= 1) contrib += __shfl_xor(contrib, o, 64);
-        if (lane == 0) red[w] = contrib;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-          float sum = 0.0f;
-          for (int q = 0; q < PT; ++q) sum += red[q];
-          dtot_part[((int64_t)c * d.H + h) * NTn + nt] = sum;
-        }
-      }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) run[v] = dec * run[v] + acc[v];
-      zero(acc);
-      ++k;
-      t0 = 0;
-    }
-  };
-
-  StateStage<PT> st0, st1, st2;
-  StepCoef cf0, cf1, cf2;
-  load_next(st0, cf0);
-  load_next(st1, cf1);
-  load_next(st2, cf2);
-  while (k < nch) {
-    step(st0, cf0);
-    if (k >= nch) break;
-    step(st1, cf1);
-    if (k >= nch) break;
-    step(st2, cf2);
+  int st = 0, s_start = 0;  // step count, step of the chunk's start
+  while (uc.k < x.nch) {
+    wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
+    lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
+    state_step<PT, FWD>(x, smem + (st % Cfg::R) * SLOT, smem + ((st + 2) % Cfg::R) * SLOT, cw + x.w * 64,
+                        s_tile + x.w * 32 * TP, hb + x.w * 1024, red, ui, uc, tot, st, s_start, acc, run);
   }
+  wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
   // final state (forward) / gradient of the initial state (backward)
   if (s_out) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int p = prow0 + acc_row(v, lane);
       if (p < d.P && n < d.N) {
-        const int64_t o = (((int64_t)sq * d.H + h) * d.P + p) * d.N + n;
+        const int64_t o = (((int64_t)sq * d.H + x.h) * d.P + p) * d.N + n;
         if (state_bf16) reinterpret_cast<bf16*>(s_out)[o] = (bf16)run[v];
         else reinterpret_cast<float*>(s_out)[o] = run[v];
       }
@@ -248,26 +347,28 @@ bool state_fused_supported(int dtype, const SsdDims& d) {
 
 int state_fused_slices(const SsdDims& d) { return d.Npad / 32; }
 
+template <int PT, bool FWD>
+static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* dt,
+                               bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
+                               hipStream_t s) {
+  const int units = d.H * d.nseq, npr = (d.Npad / 32 + 1) / 2;
+  const dim3 grid((units + 7) / 8 * 8 * npr);
+  const size_t lds = StateCfg<PT>::bytes(!FWD);
+  ensure_lds(k_state_fused<PT, FWD>, lds);
+  hipLaunchKernelGGL((k_state_fused<PT, FWD>), grid, dim3(StateCfg<PT>::NTHR), lds, s, d, b.chunks, b.seq_chunk0,
+                     b.cs, dt, u, v, hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
+}
+
 template <bool FWD>
 static hipError_t state_fused_t(const SsdDims& d, const SsdBufs& b, const void* U, const void* V, const float* dt,
                                 bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
                                 hipStream_t s) {
-  const int units = d.H * d.nseq;
-  const dim3 grid((units + 7) / 8 * 8 * (d.Npad / 32));
   const bf16* u = reinterpret_cast<const bf16*>(U);
   const bf16* v = reinterpret_cast<const bf16*>(V);
   switch (d.Ppad / 32) {
-    case 1:
-      hipLaunchKernelGGL((k_state_fused<1, FWD>), grid, dim3(64), 0, s, d, b.chunks, b.seq_chunk0, b.cs, dt, u, v,
-                         hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
-      break;
-    case 2:
-      hipLaunchKernelGGL((k_state_fused<2, FWD>), grid, dim3(128), 0, s, d, b.chunks, b.seq_chunk0, b.cs, dt, u, v,
-                         hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
-      break;
-    default:
-      hipLaunchKernelGGL((k_state_fused<4, FWD>), grid, dim3(256), 0, s, d, b.chunks, b.seq_chunk0, b.cs, dt, u, v,
-                         hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
+    case 1: state_fused_launch<1, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    case 2: state_fused_launch<2, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    default: state_fused_launch<4, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s);
   }
   return hipGetLastError();
 }

@@ -242,6 +242,59 @@ __device__ __forceinline__ void tstage_load_f32(TileStage<ROWS, W, NTHR>& s, con
   }
 }
 
+// ---------------------------------------------------------------------------
+// Unpadded tiles filled by buffer_load ... lds (whole 1 KB rows of lanes): the
+// 16-byte granules of each row are permuted instead of padding the rows.
+// ---------------------------------------------------------------------------
+// Permuted granule of logical granule g in row r of a W-wide bf16 tile.
+// Tiles read with ds_read_b64_tr_b16 (four rows, two granules per 16 lanes):
+template <int W>
+__device__ __forceinline__ int swz_tr(int r, int g) {
+  return W >= 64 ? g ^ ((r & 3) << 1) : g;
+}
+// Tiles read by rows (16 consecutive rows at one granule):
+template <int W>
+__device__ __forceinline__ int swz_nat(int r, int g) {
+  return W == 128 ? g ^ (r & 15) : (W == 64 ? g ^ ((r >> 1) & 7) : g ^ ((r >> 2) & 3));
+}
+
+// k-contiguous operand with i = mbase + L % 32 from a transposed-read tile
+// (row index k), as ttr_std does for padded tiles.
+template <int W>
+__device__ __forceinline__ bf16x4 swz_tr4(const bf16* t, int kb, int m0, int L) {
+  const int q = L & 15;
+  const int r = kb + (q >> 2), col = m0 + ((q & 3) << 2);
+  const bf16* p = t + r * W + (swz_tr<W>(r, col >> 3) << 3) + (col & 7);
+  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+template <int W>
+__device__ __forceinline__ bf16x8 swz_tr8(const bf16* t, int k0, int mbase, int L) {
+  const int h = L >> 5;
+  const int m0 = mbase + (((L >> 4) & 1) << 4);
+  return cat8(swz_tr4<W>(t, k0 + 8 * h, m0, L), swz_tr4<W>(t, k0 + 8 * h + 4, m0, L));
+}
+template <int W>
+__device__ __forceinline__ bf16x8 swz_nat8(const bf16* t, int r, int col) {
+  return *reinterpret_cast<const bf16x8*>(t + r * W + (swz_nat<W>(r, col >> 3) << 3));
+}
+
+// vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt 7, lgkmcnt 15)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0xF70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for LDS written by ds_write (lgkmcnt) and by buffer_load ... lds
+// whose writer has already retired it with its own vmcnt wait. Unlike
+// __syncthreads() (a release fence over all memory, which the compiler implements
+// as vmcnt(0): every outstanding global load, store and LDS DMA of the wave), it
+// leaves the wave's later DMAs in flight across the barrier. The "memory" clobber
+// keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // exp2 of a value already clamped; the decays below are all exp(clamp(d, -20, 20))
 // evaluated as exp2(clamp(d * log2 e, +-20 log2 e)).
 __device__ __forceinline__ float exp2_fast(float v) { return __builtin_amdgcn_exp2f(v); }
