@@ -76,8 +76,7 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const int h0 = g * d.hpg, h1 = h0 + d.hpg;
 
   // ---- one head's inputs into ring slot `slot` (kPerWave DMA instructions per wave) ----
-  auto issue = [&](int h, int slot) {
-    unsigned char* base = smem + slot * Cfg::kSlot;
+  auto issue = [&](int h, unsigned char* base) {
     const __amdgpu_buffer_rsrc_t rh = buf_rsrc(hin + ((int64_t)c * d.H + h) * Cfg::HIN);
     const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dst + ((int64_t)c * d.H + h) * Cfg::HIN);
     const int64_t xoff = (int64_t)(ci.row0 + 64 * kb) * xrow + (int64_t)h * d.P;
@@ -146,10 +145,11 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
           bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rC, ok ? (int)(t * brow + n0) * 2 : SSD_BUF_SIZE, 0, 0));
     }
   }
+  wait_vm<0>();  // the ring's waits below count the ring's DMAs only
 
   if (!brole) {
-    issue(h0, 0);
-    if (h0 + 1 < h1) issue(h0 + 1, 1);
+    issue(h0, smem);
+    if (h0 + 1 < h1) issue(h0 + 1, smem + Cfg::kSlot);
   }
   for (int h = h0; h < h1; ++h) {
     // this wave's loads of head h are done (those of h + 1 may still fly); then every wave's
@@ -157,12 +157,12 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       if (h + 1 < h1) wait_vm<Cfg::kPerWave>();
       else wait_vm<0>();
     }
-    __syncthreads();  // head h visible in LDS; slot (h + 2) % 3 is free (head h - 1 done)
-    if (!brole && h + 2 < h1) issue(h + 2, (h + 2 - h0) % 3);
+    lds_barrier();  // head h visible in LDS; slot (h + 2) % 3 is free (head h - 1 done)
+    ring_step(smem + ((h - h0) % 3) * Cfg::kSlot, smem + ((h + 2 - h0) % 3) * Cfg::kSlot, !brole && h + 2 < h1,
+              [&](unsigned char* nxt) { issue(h + 2, nxt); }, [&](const unsigned char* base) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
-    const unsigned char* base = smem + ((h - h0) % 3) * Cfg::kSlot;
     const bf16* th_ = reinterpret_cast<const bf16*>(base);
     const bf16* td_ = th_ + Cfg::HIN;
     const bf16* tx = td_ + Cfg::HIN;
@@ -202,6 +202,7 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       osum = add_xor32(osum);
       if (hh == 0 && tok) dcs_off[((int64_t)nh * MC * d.H + (int64_t)c * d.H + h) * Qpad + t] = osum * et * pt_;
     }
+    });
   }
 
   // ---- tile terms: dC += dS[kb, j] B_j (j <= kb), dB += dS[i, kb]^T C_i (i >= kb) ----

@@ -295,6 +295,18 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// One step of an LDS ring filled by buffer_load ... lds: issue(nxt) refills a free slot,
+// body(cur) consumes the current one. Passing the two slots as distinct __restrict__
+// pointers (after inlining: disjoint alias scopes on every access derived from them)
+// tells the compiler that the new DMAs do not write what the body reads, so it adds
+// no vmcnt wait of its own for them; the caller's explicit waits order the slots.
+template <typename Issue, typename Body>
+__device__ __forceinline__ void ring_step(const unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt,
+                                          bool refill, Issue&& issue, Body&& body) {
+  if (refill) issue(nxt);
+  body(cur);
+}
+
 // exp2 of a value already clamped; the decays below are all exp(clamp(d, -20, 20))
 // evaluated as exp2(clamp(d * log2 e, +-20 log2 e)).
 __device__ __forceinline__ float exp2_fast(float v) { return __builtin_amdgcn_exp2f(v); }
