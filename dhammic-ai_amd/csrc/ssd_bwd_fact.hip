@@ -78,9 +78,10 @@ struct BwdFactStage {
   Rows x, y[kSlots];
   TileStage<32 * PT, 32 * NT, kThreads> dst;
   float rcs[kSlots][PER];  // cs at this thread's staged rows of blocks j + t
-  float rdt[PER];          // dt at its staged rows of block j
+  float rdt[PER];          // dt at its staged rows of block j (as loaded: 0 where absent)
   float ecs, edt;          // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
   float cj, cl;            // cs at the last token of block j and of the chunk
+  float D;                 // the head's D (0 without D)
   int fast;
 };
 
@@ -197,11 +198,13 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   using HS = BwdFactStage<PT, NT>;
   constexpr int PER = HS::PER, RPP = kThreads / (PP / 8);  // rows of a staged tile per pass
   HS hs;
-  // dt of token tok (< Qpad) of the chunk; 1 past its end or without dt
-  auto dt_at = [&](int h, int tok) {
-    const float v = a.dt[(int64_t)(ci.row0 + min(tok, ci.len - 1)) * d.H + h];
-    return (d.has_dt && tok < ci.len) ? v : 1.0f;
-  };
+  const int r0 = min((int)threadIdx.x / (PP / 8), 63);    // first staged row of this thread
+  const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);  // token this lane finishes
+  // dt as used: the loaded value where the token exists and dt is given, else 1
+  auto dt_use = [&](float v, int tok) { return (d.has_dt && tok < ci.len) ? v : 1.0f; };
+  // All per-head loads are issued unconditionally (masked buffer loads read zeros) and
+  // used only after the staging barrier, so the compiler's wait for them stays there
+  // instead of draining the whole prefetch right after it is issued.
   auto load_head = [&](int h) {
     const int64_t xo = (int64_t)h * d.P;
     tstage_load_v(hs.x, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
@@ -212,19 +215,24 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
                       min(64, ci.len - 64 * (j + t)), d.P);
     tstage_load_v(hs.dst, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
     const float* csh = a.cs + ((int64_t)c * d.H + h) * Qpad;
-    const int r0 = min((int)threadIdx.x / (PP / 8), 63);
+    const __amdgpu_buffer_rsrc_t rcs = buf_rsrc(csh);
+    const __amdgpu_buffer_rsrc_t rdt = buf_rsrc(d.has_dt ? a.dt + (int64_t)ci.row0 * d.H + h : csh);
 #pragma unroll
     for (int t = 0; t < kSlots; ++t)
 #pragma unroll
-      for (int q = 0; q < PER; ++q) hs.rcs[t][q] = t < nt_i ? csh[64 * (j + t) + min(r0 + RPP * q, 63)] : 0.0f;
+      for (int q = 0; q < PER; ++q)
+        hs.rcs[t][q] = buf_ldf(rcs, (64 * (j + t) + min(r0 + RPP * q, 63)) * 4, t < nt_i);
 #pragma unroll
-    for (int q = 0; q < PER; ++q) hs.rdt[q] = d.has_dt ? dt_at(h, 64 * j + min(r0 + RPP * q, 63)) : 1.0f;
-    const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);
-    hs.ecs = csh[te];
-    hs.edt = d.has_dt ? dt_at(h, te) : 1.0f;
+    for (int q = 0; q < PER; ++q) {
+      const int tok = 64 * j + min(r0 + RPP * q, 63);
+      hs.rdt[q] = buf_ldf(rdt, tok * d.H * 4, d.has_dt && tok < ci.len);
+    }
+    hs.ecs = buf_ldf(rcs, te * 4, true);
+    hs.edt = buf_ldf(rdt, te * d.H * 4, d.has_dt && te < ci.len);
     hs.cj = csh[64 * j + 63];
     hs.cl = csh[Qpad - 1];
     hs.fast = a.fast[(int64_t)c * d.H + h];
+    hs.D = d.has_D ? a.Dv[h] : 0.0f;
   };
   // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
   auto flush = [&](int h) {
@@ -260,15 +268,18 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
-    __syncthreads();  // previous head: LDS reads done, reductions and ot complete
-    if (h > h_lo) flush(h - 1);
+    // previous head: LDS reads done, reductions and ot complete (LDS only: the previous
+    // head's global stores and this head's prefetch stay in flight)
+    lds_barrier();
     // row scales (zero for a flagged head): X' rows dt_s exp(c_j - cs_s), dY' rows exp(cs_l - c_j)
     {
       const bool ok = hs.fast != 0;
       const float cj2 = hs.cj * SSD_LOG2E;
       float sc[PER];
 #pragma unroll
-      for (int q = 0; q < PER; ++q) sc[q] = ok ? hs.rdt[q] * exp2_fast(cj2 - hs.rcs[0][q] * SSD_LOG2E) : 0.0f;
+      for (int q = 0; q < PER; ++q)
+        sc[q] = ok ? dt_use(hs.rdt[q], 64 * j + min(r0 + RPP * q, 63)) * exp2_fast(cj2 - hs.rcs[0][q] * SSD_LOG2E)
+                   : 0.0f;
       tstage_store_sc(hs.x, xs, sc);
 #pragma unroll
       for (int t = 0; t < kSlots; ++t)
@@ -282,11 +293,12 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     tstage_store(hs.y[0], dyu);
     tstage_store(hs.dst, dstT);
     // this head's per-token values for the finishing step (hs is reloaded below)
-    const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = hs.edt;
+    const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = dt_use(hs.edt, te);
     const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
-    __syncthreads();
+    const float Dh = hs.D;
+    if (h > h_lo) flush(h - 1);  // its LDS (ot, reductions) is not touched by the staging above
+    lds_barrier();
     if (h + 1 < h_hi) load_head(h + 1);
-    const float Dh = d.has_D ? a.Dv[h] : 0.0f;
 
     if (!xrole) {
       // ---- tiles (i, j): dS += X' dY'^T (quadrant), rowG from S * (X' dY'^T) ----
