@@ -146,7 +146,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   using Cfg = StateCfg<PT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
   const SsdDims& d = x.d;
-  const int lane = opaque_lane();
+  const int lane = threadIdx.x & 63;
   state_issue<PT, FWD>(x, nxt, ui, lane);
   const int c = uc.c;
   const int clen = uc.ci.len;
