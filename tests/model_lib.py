@@ -1,0 +1,155 @@
+"""A small Mamba-3-style language model for the model-level parity test (test scaffolding only).
+
+BASELINE config 4 is a full random-init training step of a 24-layer Mamba-3-style LM with the native SSD
+kernel swapped in, loss and per-layer gradients compared with the reference. This file restates, in plain
+PyTorch, the caller of the SSD in that model so the comparison can run at a reduced size:
+
+* ``Mamba3Block`` follows ``r2/dhammic-ai/src/mamba_base_engine.py:34-192``: one in-projection split into
+  (z, x, B, C, dt_raw, lam_raw, theta) (:62-79), the trapezoidal coefficients (:143-145), RMSNorm on B and C
+  (:148-149), per-head data-dependent RoPE of B/C with learnable per-head biases (:152-167), padding to the
+  chunk (:172-182), the two SSD calls of the trapezoidal rule sharing the first call's cache (:186-197),
+  ``+ D x`` (:199-203) and the gated output norm and projection (:206-208).
+* ``trapezoidal`` follows ``src/kernels/trapezoidal.py:6-12``; ``rope`` follows ``src/kernels/rope.py:4-10``;
+  ``rmsnorm`` follows ``src/kernels/rmsnorm.py:222-229`` (fp32 statistics, output in the input dtype).
+* The model around the blocks (pre-norm residual layers with a SwiGLU MLP, a final RMSNorm, an untied LM head
+  and token cross-entropy) is config 4's description.
+
+The SSD function is a parameter with the reference's public signature
+``ssd(x, A, B, C, chunk_size, initial_states=None, cache=None) -> (Y, final_state, cache)``, so the same model
+runs on the native drop-in or on the oracle's restatement of the reference SSD.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+def rmsnorm(x, weight, eps=1e-6):
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, d, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x):
+        return rmsnorm(x, self.weight, self.eps)
+
+
+def trapezoidal(dt_raw, lam_raw, dt_bias, A_log):
+    """(dt, dA, beta, gamma) in the dtype of dt_raw, computed in fp32."""
+    dt = F.softplus(dt_raw.float() + dt_bias.float())
+    lam = torch.sigmoid(lam_raw.float())
+    A = -torch.exp(A_log.float())
+    dA = dt * A
+    beta = (1.0 - lam) * dt * torch.exp(dA)
+    gamma = lam * dt
+    return tuple(t.to(dt_raw.dtype) for t in (dt, dA, beta, gamma))
+
+
+def rope(x, angles):
+    """Rotate (even, odd) pairs of the last axis of x by angles (..., D/2); fp32 inside, x's dtype out."""
+    xf, a = x.float(), angles.float()
+    x1, x2 = xf[..., 0::2], xf[..., 1::2]
+    c, s = torch.cos(a), torch.sin(a)
+    return torch.stack([c * x1 - s * x2, s * x1 + c * x2], dim=-1).flatten(-2).to(x.dtype)
+
+
+class Mamba3Block(nn.Module):
+    def __init__(self, ssd, d_model, d_state, expand, n_heads, chunk_size, dtype=torch.bfloat16):
+        super().__init__()
+        self.ssd = ssd
+        self.d_inner = d_model * expand
+        self.n_heads = n_heads
+        self.d_head = self.d_inner // n_heads
+        self.d_state = d_state
+        self.chunk_size = chunk_size
+        self.split_sizes = [self.d_inner, self.d_inner, d_state, d_state, n_heads, n_heads, d_state // 2]
+        self.in_proj = nn.Linear(d_model, sum(self.split_sizes), bias=False, dtype=dtype)
+        self.A_log = nn.Parameter(torch.empty(n_heads).uniform_(-4, -1))
+        self.D = nn.Parameter(torch.ones(n_heads))
+        self.dt_bias = nn.Parameter(torch.empty(n_heads).uniform_(0.001, 0.1))
+        self.B_norm = RMSNorm(d_state)
+        self.C_norm = RMSNorm(d_state)
+        self.B_bias = nn.Parameter(torch.ones(n_heads, d_state))
+        self.C_bias = nn.Parameter(torch.ones(n_heads, d_state))
+        self.out_proj = nn.Linear(self.d_inner, d_model, bias=False, dtype=dtype)
+        self.norm = RMSNorm(self.d_inner)
+
+    def forward(self, x):
+        b, T, _ = x.shape
+        x = x.to(self.in_proj.weight.dtype)
+        z, x_ssm, B_proj, C_proj, dt_raw, lam_raw, theta = torch.split(self.in_proj(x), self.split_sizes, dim=-1)
+        dt, dA, beta, gamma = trapezoidal(dt_raw, lam_raw, self.dt_bias, self.A_log)
+        B_proj = self.B_norm(B_proj)
+        C_proj = self.C_norm(C_proj)
+        cum_angles = -torch.cumsum(dt.unsqueeze(-1) * theta.unsqueeze(2), dim=1)
+        dtype = x_ssm.dtype
+        B_h = rope(B_proj.unsqueeze(2) + self.B_bias, cum_angles).to(dtype)
+        C_h = rope(C_proj.unsqueeze(2) + self.C_bias, cum_angles).to(dtype)
+        x_heads = x_ssm.reshape(b, T, self.n_heads, self.d_head)
+        pad = (self.chunk_size - T % self.chunk_size) % self.chunk_size
+        x_p = F.pad(x_heads, (0, 0, 0, 0, 0, pad))
+        dA_p = F.pad(dA, (0, 0, 0, pad))
+        B_p = F.pad(B_h, (0, 0, 0, 0, 0, pad))
+        C_p = F.pad(C_h, (0, 0, 0, 0, 0, pad))
+        gamma_p = F.pad(gamma, (0, 0, 0, pad))
+        beta_p = F.pad(beta, (0, 0, 0, pad))
+        y_gamma, _, cache = self.ssd(x_p * gamma_p.unsqueeze(-1), dA_p, B_p, C_p, self.chunk_size)
+        B_prev = F.pad(B_p[:, :-1], (0, 0, 0, 0, 1, 0))
+        x_prev = F.pad(x_p[:, :-1], (0, 0, 0, 0, 1, 0))
+        y_beta, _, _ = self.ssd(x_prev * beta_p.unsqueeze(-1), dA_p, B_prev, C_p, self.chunk_size, cache=cache)
+        y = (y_gamma + y_beta)[:, :T]
+        y = y + x_heads * self.D.to(dtype).view(1, 1, -1, 1)
+        y = self.norm(y.reshape(b, T, -1)) * F.silu(z)
+        return self.out_proj(y)
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, d_model, hidden, dtype=torch.bfloat16):
+        super().__init__()
+        self.w_gate = nn.Linear(d_model, hidden, bias=False, dtype=dtype)
+        self.w_up = nn.Linear(d_model, hidden, bias=False, dtype=dtype)
+        self.w_down = nn.Linear(hidden, d_model, bias=False, dtype=dtype)
+
+    def forward(self, x):
+        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+
+
+class Layer(nn.Module):
+    def __init__(self, ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden):
+        super().__init__()
+        self.norm1 = RMSNorm(d_model)
+        self.mixer = Mamba3Block(ssd, d_model, d_state, expand, n_heads, chunk_size)
+        self.norm2 = RMSNorm(d_model)
+        self.mlp = SwiGLU(d_model, mlp_hidden)
+
+    def forward(self, h):
+        h = h + self.mixer(self.norm1(h))
+        return h + self.mlp(self.norm2(h))
+
+
+class Mamba3LM(nn.Module):
+    def __init__(self, ssd, vocab, d_model, n_layers, d_state, expand, n_heads, chunk_size, mlp_hidden):
+        super().__init__()
+        self.embed = nn.Embedding(vocab, d_model, dtype=torch.bfloat16)
+        self.layers = nn.ModuleList(
+            [Layer(ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden) for _ in range(n_layers)])
+        self.norm_f = RMSNorm(d_model)
+        self.lm_head = nn.Linear(d_model, vocab, bias=False, dtype=torch.bfloat16)
+
+    def loss(self, tokens, targets):
+        h = self.embed(tokens)
+        for layer in self.layers:
+            h = layer(h)
+        logits = self.lm_head(self.norm_f(h))
+        return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), targets.reshape(-1))
+
+
+def set_ssd(model, ssd):
+    for layer in model.layers:
+        layer.mixer.ssd = ssd
