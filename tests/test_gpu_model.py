@@ -1,6 +1,7 @@
 """Model-level parity, BASELINE config 4's check at a reduced size: one training step (loss and every
 parameter's gradient) of a Mamba-3-style LM (tests/model_lib.py) with the native SSD swapped in, against the
-same model, weights and tokens with the oracle's restatement of the reference SSD.
+same model, weights and tokens with the oracle's restatement of the reference SSD. Two sizes: two small layers
+on a sequence that is not a chunk multiple, and one layer at config 4's exact layer shape.
 
 Both runs share every op outside the SSD (bf16 weights and activations, as the reference block runs), so the
 differences come from the SSD alone: the native kernel computes in bf16 with fp32 accumulation, the oracle in
@@ -11,9 +12,12 @@ path's A gradient in both) on a sequence that is not a chunk multiple, so they a
 Tolerances (normwise, max|got - ref| / max|ref| per tensor): the loss to 1e-3. A model-level gradient sums the
 whole step's products, and bf16 rounding inside the SSD moves it by several times the per-op 1e-2 bound: the
 reference itself, run with bf16 intermediates as it does on bf16 inputs (the oracle in bf16), deviates from the
-fp32 math by up to about 8e-2 on the first layer's in-projection. So each native gradient must stay within
-twice the reference's own bf16 deviation for that tensor, and never needs to beat 2e-2. A kernel mistake (a
-dropped term, a wrong cache path) moves gradients by O(1), far outside either bound.
+fp32 math by up to about 8e-2 on the in-projection gradient of the small model, and by up to 0.37 at config 4's
+layer shape, where the RoPE angles accumulate over 4096 tokens and bf16 rounding of the SSD's inputs and outputs
+is amplified through them. So each native gradient must stay within twice the reference's own bf16 deviation for
+that tensor, and never needs to beat 2e-2. The SSD-facing gradients (A_log, D, the B/C biases and norms) stay
+within 1.3e-2 at config 4's shape. On the CPU the check fails for a dropped dA gradient and for a beta call that
+ignores the cache (A_log off by 0.5-1.0).
 """
 from __future__ import annotations
 
@@ -53,14 +57,21 @@ def _step(model, tokens, targets):
     return loss.detach().double().item(), {n: p.grad.detach().clone() for n, p in model.named_parameters()}
 
 
-def test_mamba3_lm_training_step_native_ssd_matches_reference_ssd():
+# config 4's layer: d_model 1024, expand 2 (H = 32, P = 64), N = 128, per-head B/C, B = 4, L = 4096; one layer
+# and a small vocabulary (the LM head is not what is checked)
+SIZES_CFG4_LAYER = dict(vocab=2048, d_model=1024, n_layers=1, d_state=128, expand=2, n_heads=32, chunk_size=256,
+                        mlp_hidden=2048)
+
+
+@pytest.mark.parametrize("sizes,b,T", [(SIZES, 2, 384), (SIZES_CFG4_LAYER, 4, 4096)],
+                         ids=["small_two_layers_padded", "config4_layer_shape"])
+def test_mamba3_lm_training_step_native_ssd_matches_reference_ssd(sizes, b, T):
     import kernels
     torch.manual_seed(0)
-    model = Mamba3LM(kernels.fused_ssd_scan, **SIZES).to(DEV)
+    model = Mamba3LM(kernels.fused_ssd_scan, **sizes).to(DEV)
     g = torch.Generator().manual_seed(1)
-    b, T = 2, 384  # 1.5 chunks: the blocks pad to 512
-    tokens = torch.randint(0, SIZES["vocab"], (b, T), generator=g).to(DEV)
-    targets = torch.randint(0, SIZES["vocab"], (b, T), generator=g).to(DEV)
+    tokens = torch.randint(0, sizes["vocab"], (b, T), generator=g).to(DEV)
+    targets = torch.randint(0, sizes["vocab"], (b, T), generator=g).to(DEV)
 
     loss_n, grads_n = _step(model, tokens, targets)
     set_ssd(model, reference_ssd)
