@@ -301,7 +301,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     if (h + 1 < h_hi) load_head(h + 1);
 
     if (!xrole) {
-      // ---- tiles (i, j): dS += X' dY'^T (quadrant), rowG from S * (X' dY'^T) ----
+      // ---- tiles (i, j): X' dY'^T (quadrant) into dS, rowG from S * (X' dY'^T) ----
 #pragma unroll
       for (int t = 0; t < kSlots; ++t) {
         if (t >= nt_i) continue;
@@ -310,12 +310,11 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           floatx16 tq;
           zero(tq);
 #pragma unroll
-          for (int kk = 0; kk < PP / 16; ++kk) {
-            const bf16x8 av = tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh);
-            const bf16x8 bv = tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh);
-            mfma(dS[t], av, bv);
-            mfma(tq, av, bv);
-          }
+          for (int kk = 0; kk < PP / 16; ++kk)
+            mfma(tq, tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh), tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh));
+          // this head's X' dY'^T: into the head-summed dS, and G over the quadrant
+#pragma unroll
+          for (int v = 0; v < 16; ++v) dS[t][v] += tq[v];
           // G over the quadrant: lane l holds column l, registers the s rows (S^T read back
           // from LDS in that layout, four rows per transposed read)
           float rs = 0.0f;
