@@ -263,8 +263,12 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     }
   };
 
-  load_head(h_lo);
-  for (int h = h_lo; h < h_hi; ++h) {
+  // head order rotated per chunk: the resident blocks then read different 128-byte columns of the 8 KB
+  // token rows at any moment instead of all the same one (HBM channel spread)
+  const int nh = h_hi - h_lo, hrot = c % nh;
+  auto head = [&](int k) { const int m = k + hrot; return h_lo + (m >= nh ? m - nh : m); };
+  load_head(head(0));
+  for (int k = 0; k < nh; ++k) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
@@ -296,9 +300,9 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = dt_use(hs.edt, te);
     const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
     const float Dh = hs.D;
-    if (h > h_lo) flush(h - 1);  // its LDS (ot, reductions) is not touched by the staging above
+    if (k > 0) flush(head(k - 1));  // its LDS (ot, reductions) is not touched by the staging above
     lds_barrier();
-    if (h + 1 < h_hi) load_head(h + 1);
+    if (k + 1 < nh) load_head(head(k + 1));
 
     if (!xrole) {
       // ---- tiles (i, j): X' dY'^T (quadrant) into dS, rowG from S * (X' dY'^T) ----
@@ -397,7 +401,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     }
   }
   __syncthreads();
-  flush(h_hi - 1);
+  flush(head(nh - 1));
 
   // ---- dS tiles, summed over the slice's heads (zero outside the causal mask) ----
   if (xrole) return;

@@ -147,19 +147,25 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   }
   wait_vm<0>();  // the ring's waits below count the ring's DMAs only
 
+  // head order rotated per chunk (the blocks of one chunk keep the same order, so they still share each
+  // head's tiles through L2): the resident blocks then read different 128-byte columns of the 8 KB token
+  // rows at any moment instead of all the same one (HBM channel spread)
+  const int nhd = h1 - h0, hrot = c % nhd;
+  auto head = [&](int k) { const int m = k + hrot; return h0 + (m >= nhd ? m - nhd : m); };
   if (!brole) {
-    issue(h0, smem);
-    if (h0 + 1 < h1) issue(h0 + 1, smem + Cfg::kSlot);
+    issue(head(0), smem);
+    if (1 < nhd) issue(head(1), smem + Cfg::kSlot);
   }
-  for (int h = h0; h < h1; ++h) {
-    // this wave's loads of head h are done (those of h + 1 may still fly); then every wave's
+  for (int k = 0; k < nhd; ++k) {
+    const int h = head(k);
+    // this wave's loads of head k are done (those of k + 1 may still fly); then every wave's
     if (!brole) {
-      if (h + 1 < h1) wait_vm<Cfg::kPerWave>();
+      if (k + 1 < nhd) wait_vm<Cfg::kPerWave>();
       else wait_vm<0>();
     }
-    lds_barrier();  // head h visible in LDS; slot (h + 2) % 3 is free (head h - 1 done)
-    ring_step(smem + ((h - h0) % 3) * Cfg::kSlot, smem + ((h + 2 - h0) % 3) * Cfg::kSlot, !brole && h + 2 < h1,
-              [&](unsigned char* nxt) { issue(h + 2, nxt); }, [&](const unsigned char* base) {
+    lds_barrier();  // head k visible in LDS; slot (k + 2) % 3 is free (head k - 1 done)
+    ring_step(smem + (k % 3) * Cfg::kSlot, smem + ((k + 2) % 3) * Cfg::kSlot, !brole && k + 2 < nhd,
+              [&](unsigned char* nxt) { issue(head(k + 2), nxt); }, [&](const unsigned char* base) {
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
