@@ -30,6 +30,12 @@ CFLAGS = [
     f"-I{PKG.parent / 'include'}",
 ]
 
+# Files whose loops carry an MFMA accumulator through VALU code (the state walks' chunk-end update, the
+# forward scan's per-head epilogue): with the default AGPR form the compiler copies the accumulator
+# between AGPRs and VGPRs on every iteration (16 + 16 moves per 32 x 32 tile); the VGPR form keeps it in
+# place. Not global: the fp32 forward kernel spills with it.
+MFMA_VGPR_FORM = {"ssd_state_fused.hip", "ssd_scan_fwd_fact.hip"}
+
 
 def _run(cmd, verbose):
     if verbose:
@@ -49,7 +55,8 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
 
     def compile_one(pair):
         src, obj = pair
-        _run([HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)], verbose)
+        extra = ["-mllvm", "-amdgpu-mfma-vgpr-form"] if src.name in MFMA_VGPR_FORM else []
+        _run([HIPCC, *CFLAGS, *extra, "-c", str(src), "-o", str(obj)], verbose)
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(compile_one, zip(sources, objs)))
