@@ -12,9 +12,11 @@
 // and dinit = run. The running state stays in the MFMA accumulator registers;
 // nothing but hin / dst (bf16) and the final / initial state is written.
 //
-// One block per (pair of 32-wide n tiles, head, sequence) with one wave per
-// (32-wide p tile, n tile of the pair); wave w owns the 32 x 32 state tile
-// (p tile w % PT, n tile w / PT). Blocks of one (head, sequence) are numbered
+// One block per (pair of 32-wide n tiles, head, sequence) with 2 PT waves. In the
+// forward walk with head dims 33..64 (PT = 2) wave w owns all 64 rows p of the 16
+// columns 16 w .. 16 w + 15 of the pair (four 16 x 16 MFMA tiles), so each B element
+// is scaled by the per-token factor once per block; otherwise wave w owns the
+// 32 x 32 tile (p tile w % PT, n tile w / PT). Blocks of one (head, sequence) are numbered
 // onto one XCD (same block index mod 8) so their shared x / dy rows come from
 // HBM once. Tokens go 64 at a time through a ring of three LDS slots filled by
 // buffer_load ... lds (x or dy rows, the pair's B or C columns, cs and dt),
@@ -41,11 +43,32 @@ struct StateCfg {
   static constexpr int PERW = (UI + VI) / NW;   // row DMAs per wave and step
   static constexpr int D = PERW + 1;            // DMAs per wave and step (+ one scalar row)
   static_assert((UI + VI) % NW == 0, "DMA split");
-  static constexpr int TP = 40;                 // s_tile row pitch (elements)
+  static constexpr int TP = 40;                 // s_tile row pitch (elements), 32 x 32 tiles
+  // PT = 2: each wave owns all 64 p of 16 columns of the pair (four 16 x 16 MFMA tiles), so every
+  // B / C element is scaled by one wave, not by both p-tile waves; other PT use 32 x 32 tiles
+  static constexpr int TW = 24;                 // s_tile row pitch (elements), 64 x 16 tiles
+  static constexpr int TWE = PT == 2 ? 64 * TW : 32 * TP;  // s_tile elements per wave
   static size_t bytes(bool bwd) {
-    return (size_t)R * SLOT + NW * 64 * 4 + NW * 32 * TP * 2 + (bwd ? NW * 2048 : 0) + 64;
+    return (size_t)R * SLOT + NW * 64 * 4 + NW * TWE * 2 + (bwd ? NW * 2048 : 0) + 64;
   }
 };
+
+// Whether the walk uses the 64 x 16 wave tiles: the forward walk at PT = 2. The backward walk
+// keeps 32 x 32 tiles: with 64 x 16 it ran 11 us slower at config 2 on the same box (199 against
+// 188 us) despite 25 % fewer VALU instructions, while the forward walk gained 6-10 us.
+template <int PT, bool FWD>
+constexpr bool state_wide() {
+  return PT == 2 && FWD;
+}
+// Row (p, within the wave's tile) of accumulator register v, and column (n) of lane L.
+template <bool WIDE>
+__device__ __forceinline__ int state_row(int v, int L) {
+  return WIDE ? 16 * (v >> 2) + 4 * (L >> 4) + (v & 3) : acc_row(v, L);
+}
+template <bool WIDE>
+__device__ __forceinline__ int state_col(int L) {
+  return WIDE ? (L & 15) : (L & 31);
+}
 
 }  // namespace
 
@@ -62,6 +85,7 @@ struct StateCtx {
   float* dtot_part;
   int64_t urow, vrow, ucol, vcol;
   int h, np, w, pt, ntl, nt, NTn, c0, c1, nch;
+  int ncol0;  // first state column (n) of this wave's tile
   bool nt_ok;
 };
 
@@ -145,6 +169,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
                                            floatx16& acc, floatx16& run) {
   using Cfg = StateCfg<PT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
+  constexpr bool WIDE = state_wide<PT, FWD>();
   const SsdDims& d = x.d;
   const int lane = threadIdx.x & 63;
   state_issue<PT, FWD>(x, nxt, ui, lane);
@@ -153,31 +178,34 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   int& t0 = uc.t;
   const int64_t soff = ((int64_t)c * d.H + x.h) * d.Ppad * d.Npad;
   const int prow0 = 32 * x.pt;
+  // tile geometry: rows (p) x columns (n) per wave, and the 16-byte pieces per row
+  constexpr int TR = WIDE ? 64 : 32, TC = WIDE ? 16 : 32, TPR = WIDE ? Cfg::TW : TP;
+  constexpr int GPR = TC / 8;
   if (t0 == 0) {
     s_start = st;
     // state entering (forward) / gradient leaving (backward) chunk c: accumulator layout
-    // -> this wave's LDS tile -> 16-byte row pieces (16 rows x 64 bytes per store)
+    // -> this wave's LDS tile -> 16-byte row pieces (two per lane)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) tw[acc_row(v, lane) * TP + (lane & 31)] = (bf16)run[v];
+    for (int v = 0; v < 16; ++v) tw[state_row<WIDE>(v, lane) * TPR + state_col<WIDE>(lane)] = (bf16)run[v];
     __builtin_amdgcn_wave_barrier();
     if (x.nt_ok) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int id = lane + 64 * q, r = id >> 2, c8 = (id & 3) * 8;
-        const int64_t o = soff + (int64_t)(prow0 + r) * d.Npad + 32 * x.nt + c8;
-        *reinterpret_cast<bf16x8*>(x.hst + o) = *reinterpret_cast<const bf16x8*>(tw + r * TP + c8);
+        const int id = lane + 64 * q, r = id / GPR, c8 = (id % GPR) * 8;
+        const int64_t o = soff + (int64_t)(prow0 + r) * d.Npad + x.ncol0 + c8;
+        *reinterpret_cast<bf16x8*>(x.hst + o) = *reinterpret_cast<const bf16x8*>(tw + r * TPR + c8);
       }
     }
     __builtin_amdgcn_wave_barrier();
     if (!FWD) {
-      // this wave's 32 x 32 tile of h_in[c], consumed at the end of the chunk
+      // this wave's tile of h_in[c] ([TR][TC], 2 KB), consumed at the end of the chunk
       const __amdgpu_buffer_rsrc_t rh = buf_rsrc(x.hin_in + soff);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int r = 16 * q + lane / 4, c8 = (lane % 4) * 8;
+        const int r = (TR / 2) * q + lane / GPR, c8 = (lane % GPR) * 8;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rh, (__attribute__((address_space(3))) void*)(hbw + q * 512), 16,
-            x.nt_ok ? (int)(((prow0 + r) * d.Npad + 32 * x.nt + c8) * 2) : SSD_BUF_SIZE, 0, 0, 0);
+            x.nt_ok ? (int)(((prow0 + r) * d.Npad + x.ncol0 + c8) * 2) : SSD_BUF_SIZE, 0, 0, 0);
       }
     }
   }
@@ -191,17 +219,36 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
     const float f = FWD ? exp_clamp(tot - cst) * dtt : exp_clamp(cst);
     cw[lane] = t0 + lane < clen ? f : 0.0f;
   }
+  if constexpr (WIDE) {
+    // 64 p x 16 n: the scaled B / C operand is shared by the four p blocks
 #pragma unroll
-  for (int kk = 0; kk < 64; kk += 16) {
-    const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5));
-    const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5) + 4);
-    bf16x8 b = swz_tr8<64>(tv, kk, 32 * x.ntl, lane);
+    for (int kk = 0; kk < 64; kk += 32) {
+      const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 4));
+      const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 4) + 4);
+      bf16x8 b = swz_tr8_16<64>(tv, kk, 16 * x.w, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      b[e] = (bf16)((float)b[e] * f0[e]);
-      b[4 + e] = (bf16)((float)b[4 + e] * f1[e]);
+      for (int e = 0; e < 4; ++e) {
+        b[e] = (bf16)((float)b[e] * f0[e]);
+        b[4 + e] = (bf16)((float)b[4 + e] * f1[e]);
+      }
+      mfma16<0>(acc, swz_tr8_16<PP>(tu, kk, 0, lane), b);
+      mfma16<1>(acc, swz_tr8_16<PP>(tu, kk, 16, lane), b);
+      mfma16<2>(acc, swz_tr8_16<PP>(tu, kk, 32, lane), b);
+      mfma16<3>(acc, swz_tr8_16<PP>(tu, kk, 48, lane), b);
     }
-    mfma(acc, swz_tr8<PP>(tu, kk, prow0, lane), b);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 64; kk += 16) {
+      const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5));
+      const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5) + 4);
+      bf16x8 b = swz_tr8<64>(tv, kk, 32 * x.ntl, lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b[e] = (bf16)((float)b[e] * f0[e]);
+        b[4 + e] = (bf16)((float)b[4 + e] * f1[e]);
+      }
+      mfma(acc, swz_tr8<PP>(tu, kk, prow0, lane), b);
+    }
   }
   t0 += 64;
   ++st;
@@ -219,12 +266,16 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
       }
       float contrib = 0.0f;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hbw[acc_row(v, lane) * 32 + (lane & 31)];
+      for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hbw[state_row<WIDE>(v, lane) * TC + state_col<WIDE>(lane)];
       contrib *= dec * clamp_pass(tot);
       contrib = wave_sum(contrib);
       if (lane == 0) red[x.w] = contrib;
       lds_barrier();
-      if (x.nt_ok && x.pt == 0 && lane == 0) {
+      // one partial per 32-wide n tile: the PT waves of a 32 x 32 column, or the two 16-wide waves
+      if constexpr (WIDE) {
+        if (x.nt_ok && (x.w & 1) == 0 && lane == 0)
+          x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn + x.nt] = red[x.w] + red[x.w + 1];
+      } else if (x.nt_ok && x.pt == 0 && lane == 0) {
         float sum = 0.0f;
         for (int q = 0; q < PT; ++q) sum += red[x.ntl * PT + q];
         x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn + x.nt] = sum;
@@ -251,10 +302,11 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
                                                          int state_bf16, float* __restrict__ dtot_part) {
   using Cfg = StateCfg<PT>;
   constexpr int TP = Cfg::TP, SLOT = Cfg::SLOT;
+  constexpr bool WIDE = state_wide<PT, FWD>();
   extern __shared__ __align__(16) unsigned char smem[];
   float* cw = reinterpret_cast<float*>(smem + Cfg::R * SLOT);             // [NW][64] per-token factors
-  bf16* s_tile = reinterpret_cast<bf16*>(cw + Cfg::NW * 64);              // [NW][32][TP]
-  bf16* hb = s_tile + Cfg::NW * 32 * TP;                                  // [NW][32][32] (backward: h_in)
+  bf16* s_tile = reinterpret_cast<bf16*>(cw + Cfg::NW * 64);              // [NW][TWE] state tiles
+  bf16* hb = s_tile + Cfg::NW * Cfg::TWE;                                 // [NW][1024] (backward: h_in)
   float* red = reinterpret_cast<float*>(hb + (FWD ? 0 : Cfg::NW * 1024)); // [NW]
 
   // block -> (n tile pair, unit = (head, sequence)); the pairs of a unit share an XCD
@@ -270,9 +322,16 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
   const int sq = unit / d.H;
   const int g = x.h / d.hpg;
   x.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  x.pt = x.w % PT;
-  x.ntl = x.w / PT;
-  x.nt = 2 * x.np + x.ntl;
+  if constexpr (WIDE) {  // wave w: all p, columns 16 w .. 16 w + 15 of the pair
+    x.pt = 0;
+    x.ntl = x.w >> 1;
+    x.ncol0 = 64 * x.np + 16 * x.w;
+  } else {                    // wave w: p tile w % PT, 32-wide column tile w / PT of the pair
+    x.pt = x.w % PT;
+    x.ntl = x.w / PT;
+    x.ncol0 = 64 * x.np + 32 * x.ntl;
+  }
+  x.nt = x.ncol0 / 32;
   x.nt_ok = x.nt < x.NTn;
   x.chunks = chunks;
   x.cs = cs;
@@ -287,7 +346,7 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
   x.ucol = (int64_t)x.h * d.P;
   x.vcol = (int64_t)g * d.N + 64 * x.np;
   const int lane = threadIdx.x & 63;
-  const int n = 32 * x.nt + (lane & 31);
+  const int n = x.ncol0 + state_col<WIDE>(lane);
   const int prow0 = 32 * x.pt;
 
   // running state: rows p = 32 pt + acc_row(v), column n
@@ -296,7 +355,7 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
   if (s_in) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int p = prow0 + acc_row(v, lane);
+      const int p = prow0 + state_row<WIDE>(v, lane);
       if (p < d.P && n < d.N) {
         const int64_t o = (((int64_t)sq * d.H + x.h) * d.P + p) * d.N + n;
         run[v] = state_bf16 ? (float)reinterpret_cast<const bf16*>(s_in)[o] : reinterpret_cast<const float*>(s_in)[o];
@@ -324,14 +383,14 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
     wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
     lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
     state_step<PT, FWD>(x, smem + (st % Cfg::R) * SLOT, smem + ((st + 2) % Cfg::R) * SLOT, cw + x.w * 64,
-                        s_tile + x.w * 32 * TP, hb + x.w * 1024, red, ui, uc, tot, st, s_start, acc, run);
+                        s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, ui, uc, tot, st, s_start, acc, run);
   }
   wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
   // final state (forward) / gradient of the initial state (backward)
   if (s_out) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int p = prow0 + acc_row(v, lane);
+      const int p = prow0 + state_row<WIDE>(v, lane);
       if (p < d.P && n < d.N) {
         const int64_t o = (((int64_t)sq * d.H + x.h) * d.P + p) * d.N + n;
         if (state_bf16) reinterpret_cast<bf16*>(s_out)[o] = (bf16)run[v];

@@ -124,6 +124,16 @@ __device__ __forceinline__ void mfma(floatx16& acc, const bf16x8& a, const bf16x
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
 }
 
+// 16 x 16 x 32 product into registers 4 I .. 4 I + 3 of acc (lane L holds column L % 16,
+// rows 4 (L / 16) + 0..3 of the 16 x 16 tile).
+template <int I>
+__device__ __forceinline__ void mfma16(floatx16& acc, const bf16x8& a, const bf16x8& b) {
+  floatx4 c = __builtin_shufflevector(acc, acc, 4 * I, 4 * I + 1, 4 * I + 2, 4 * I + 3);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[4 * I + e] = c[e];
+}
+
 // ---------------------------------------------------------------------------
 // Global -> LDS staging of a ROWS x W bf16 tile from a row-major tensor, with
 // rows >= nrows and columns >= width zero-filled. Thread t handles 16-byte
@@ -273,6 +283,12 @@ __device__ __forceinline__ bf16x8 swz_tr8(const bf16* t, int k0, int mbase, int 
   const int h = L >> 5;
   const int m0 = mbase + (((L >> 4) & 1) << 4);
   return cat8(swz_tr4<W>(t, k0 + 8 * h, m0, L), swz_tr4<W>(t, k0 + 8 * h + 4, m0, L));
+}
+// The same for the 16 x 16 x 32 MFMA operand layout: i = mbase + L % 16, k = k0 + 8 (L / 16) + 0..7.
+template <int W>
+__device__ __forceinline__ bf16x8 swz_tr8_16(const bf16* t, int k0, int mbase, int L) {
+  const int kb = k0 + 8 * (L >> 4);
+  return cat8(swz_tr4<W>(t, kb, mbase, L), swz_tr4<W>(t, kb + 4, mbase, L));
 }
 template <int W>
 __device__ __forceinline__ bf16x8 swz_nat8(const bf16* t, int r, int col) {

@@ -217,11 +217,13 @@ def test_extended_bf16_gated_130m_slice():
     _check_ext(SsdShape(2, 1024, 6, 64, 1, 128, 256), torch.bfloat16, with_z=True, seed=11)
 
 
-@pytest.mark.parametrize("P,N", [(128, 48), (32, 96)])
+@pytest.mark.parametrize("P,N", [(128, 48), (32, 96), (64, 96), (48, 32)])
 def test_extended_bf16_wide_head_odd_state_tiles(P, N):
     """Head widths and state sizes at the edges of the tiled kernels: P = 128 (eight waves per state
     walk, the widest p tiling) with N = 48 (two 32-wide n tiles, the second half empty), and P = 32 with
-    N = 96 (an n-tile pair whose second tile lies past N). bf16 with init / dfinal."""
+    N = 96 (an n-tile pair whose second tile lies past N). The state walks' 64 x 16 wave tiles (head dims
+    33..64): P = 64 with N = 96 (two of a pair's four waves past N) and P = 48 with N = 32 (padded rows p,
+    a single 32-wide n tile). bf16 with init / dfinal."""
     _check_ext(SsdShape(2, 768, 4, P, 1, N, 256), torch.bfloat16, with_z=False, seed=17 + P)
 
 
