@@ -21,9 +21,28 @@ hipError_t launch_bwd_row(int dtype, const SsdDims& d, const SsdBufs& b, const S
 // ---------------------------------------------------------------------------
 // Finish: dcs per position, da = reverse in-chunk cumsum (the adjoint of the
 // inclusive cumsum, ssd_scan.py:368), then ddt / per-token dA / dA partials.
-// One wave per (chunk, head).
+// One wave per (chunk, head); lane L owns the PER = Qpad / 64 consecutive positions
+// PER L .. PER L + PER - 1 and reads them with one load per array (with PER
+// separate dword loads, the lines of the ~10 MB in flight per XCD were evicted
+// between them and fetched up to four times).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <int PER>
+__device__ __forceinline__ void ld_per(const float* __restrict__ p, float (&o)[PER]) {
+  if constexpr (PER == 4) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = v[e];
+  } else if constexpr (PER == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    o[0] = v.x;
+    o[1] = v.y;
+  } else {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] = p[e];
+  }
+}
+
+template <typename T, int PER>
 __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const ChunkInfo* __restrict__ chunks,
                                                     const float* __restrict__ Ah, const float* __restrict__ dt,
                                                     float* __restrict__ ddt, T* __restrict__ dA_tok) {
@@ -37,31 +56,45 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
     if (lane == 0) bf.dA_part[ch] = 0.0f;
     return;
   }
-  const int per = d.Qpad / 64;
+  constexpr int per = PER;
   const int64_t base = ch * d.Qpad;
-  float v[4];
+  const int64_t pstride = (int64_t)d.max_chunks * d.H * d.Qpad;  // between partial arrays
+  const int l0 = lane * PER;
+  float v[PER], t[PER];
   float esum = 0.0f;
-  for (int e = 0; e < per; ++e) {
-    const int l = lane * per + e;
-    float x = 0.0f;
-    if (l < ci.len) {
-      // rowG partial k covers the rows of blocks >= k (column set k of the fused
-      // path starts at column block k); the column / row path writes one partial
-      float rg = 0.0f;
-      for (int k = 0; k < bf.nrowg && k <= l / 64; ++k)
-        rg += bf.rowG[(int64_t)k * d.max_chunks * d.H * d.Qpad + base + l];
-      float off = 0.0f;
-      for (int k = 0; k < bf.ndcs; ++k) off += bf.dcs_off[(int64_t)k * d.max_chunks * d.H * d.Qpad + base + l];
-      x = rg - bf.colG[base + l] + off - bf.eterm[base + l];
-      esum += bf.eterm[base + l];
+  {
+    // rowG partial k covers the rows of blocks >= k (column set k of the fused path starts at
+    // column block k); the column / row path writes one partial. A lane's positions share a block.
+    float x[PER];
+    ld_per<PER>(bf.rowG + base + l0, x);
+    for (int k = 1; k < bf.nrowg && k <= l0 / 64; ++k) {
+      ld_per<PER>(bf.rowG + k * pstride + base + l0, t);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[e] += t[e];
     }
-    v[e] = x;
+    for (int k = 0; k < bf.ndcs; ++k) {
+      ld_per<PER>(bf.dcs_off + k * pstride + base + l0, t);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[e] += t[e];
+    }
+    ld_per<PER>(bf.colG + base + l0, t);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) x[e] -= t[e];
+    ld_per<PER>(bf.eterm + base + l0, t);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const bool ok = l0 + e < ci.len;
+      v[e] = ok ? x[e] - t[e] : 0.0f;
+      esum += ok ? t[e] : 0.0f;
+    }
   }
   for (int o = 32; o > 0; o >>= 1) esum += __shfl_xor(esum, o, 64);
   float dtot = 0.0f;
   for (int k = 0; k < bf.npass_blk; ++k) dtot += bf.dtot_part[ch * bf.npass_blk + k];
   const int last = ci.len - 1;
-  if (last / per == lane) v[last % per] += esum + dtot;
+#pragma unroll
+  for (int e = 0; e < per; ++e)
+    if (l0 + e == last) v[e] += esum + dtot;
   // reverse inclusive scan: local suffix, then exclusive suffix of lane totals
   float run = 0.0f;
   for (int e = per - 1; e >= 0; --e) {
@@ -75,14 +108,16 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
   }
   const float excl = incl - run;
   float dAp = 0.0f;
+  if (d.a_mode == 0 && ddt && d.has_dt) ld_per<PER>(bf.xdx + base + l0, t);
+#pragma unroll
   for (int e = 0; e < per; ++e) {
-    const int l = lane * per + e;
+    const int l = l0 + e;
     if (l >= ci.len) continue;
     const float da = v[e] + excl;
     const int64_t row = ci.row0 + l;
     if (d.a_mode == 0) {
       const float dtv = d.has_dt ? dt[row * d.H + h] : 1.0f;
-      if (ddt && d.has_dt) ddt[row * d.H + h] = bf.xdx[base + l] + Ah[h] * da;
+      if (ddt && d.has_dt) ddt[row * d.H + h] = t[e] + Ah[h] * da;
       dAp += dtv * da;
     } else if (d.a_mode == 1) {
       if (dA_tok) dA_tok[row * d.H + h] = from_f<T>(da);
@@ -111,15 +146,26 @@ size_t lds_bwd_row(int dtype, const SsdDims& d) {
   return fixed + (regA > regB ? regA : regB);
 }
 
+template <int PER>
+static void bwd_finish_launch(int dtype, dim3 grid, const SsdDims& d, const SsdBufs& b, const float* Ah,
+                              const float* dt, float* ddt, void* dA_tok, hipStream_t s) {
+  if (dtype == 1)
+    hipLaunchKernelGGL((k_bwd_finish<bf16, PER>), grid, dim3(256), 0, s, d, b, b.chunks, Ah, dt, ddt,
+                       reinterpret_cast<bf16*>(dA_tok));
+  else
+    hipLaunchKernelGGL((k_bwd_finish<float, PER>), grid, dim3(256), 0, s, d, b, b.chunks, Ah, dt, ddt,
+                       reinterpret_cast<float*>(dA_tok));
+}
+
 hipError_t launch_bwd_finish(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in, float* ddt,
                              void* dA_tok, hipStream_t s) {
   dim3 grid(d.max_chunks, (d.H + 3) / 4);
   const float* Ah = d.a_mode == 0 ? reinterpret_cast<const float*>(in.A) : nullptr;
-  if (dtype == 1)
-    hipLaunchKernelGGL(k_bwd_finish<bf16>, grid, dim3(256), 0, s, d, b, b.chunks, Ah, in.dt, ddt,
-                       reinterpret_cast<bf16*>(dA_tok));
-  else
-    hipLaunchKernelGGL(k_bwd_finish<float>, grid, dim3(256), 0, s, d, b, b.chunks, Ah, in.dt, ddt,
-                       reinterpret_cast<float*>(dA_tok));
+  switch (d.Qpad / 64) {
+    case 1: bwd_finish_launch<1>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
+    case 2: bwd_finish_launch<2>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
+    case 3: bwd_finish_launch<3>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
+    default: bwd_finish_launch<4>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s);
+  }
   return hipGetLastError();
 }
