@@ -65,20 +65,21 @@ hipError_t launch_reduce_heads(const SsdDims& d, const SsdBufs& b, float* dA_hea
   return hipGetLastError();
 }
 
-// out[k] = sum_b part[b][k]: block of 1024 threads = 64 columns x 16 row
-// groups; row group g sums rows g, g + 16, ... in order, then the group sums
-// are added in a fixed tree order (deterministic).
+// out[k] = sum_b part[b][k]: block of 1024 threads = 16 columns x 64 row groups
+// (width / 16 blocks, so a 4096-wide row fills the chip); row group g sums rows
+// g, g + 64, ... in order, then the group sums are added in a fixed tree order
+// (deterministic).
 __global__ void __launch_bounds__(1024) k_reduce_rows(int nblocks, int width, const float* __restrict__ part,
                                                       float* __restrict__ out) {
-  __shared__ float red[16][64];
-  const int col = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int k = blockIdx.x * 64 + col;
+  __shared__ float red[64][16];
+  const int col = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int k = blockIdx.x * 16 + col;
   float acc = 0.0f;
   if (k < width)
-    for (int b = grp; b < nblocks; b += 16) acc += part[(int64_t)b * width + k];
+    for (int b = grp; b < nblocks; b += 64) acc += part[(int64_t)b * width + k];
   red[grp][col] = acc;
   __syncthreads();
-  for (int o = 8; o > 0; o >>= 1) {
+  for (int o = 32; o > 0; o >>= 1) {
     if (grp < o) red[grp][col] += red[grp + o][col];
     __syncthreads();
   }
@@ -86,6 +87,6 @@ __global__ void __launch_bounds__(1024) k_reduce_rows(int nblocks, int width, co
 }
 
 hipError_t launch_reduce_rows(int nblocks, int width, const float* part, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(k_reduce_rows, dim3((width + 63) / 64), dim3(1024), 0, s, nblocks, width, part, out);
+  hipLaunchKernelGGL(k_reduce_rows, dim3((width + 15) / 16), dim3(1024), 0, s, nblocks, width, part, out);
   return hipGetLastError();
 }
