@@ -46,15 +46,30 @@ template <typename T, int PER>
 __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const ChunkInfo* __restrict__ chunks,
                                                     const float* __restrict__ Ah, const float* __restrict__ dt,
                                                     float* __restrict__ ddt, T* __restrict__ dA_tok) {
+  // dt / ddt of the block's four heads are 16 contiguous bytes per position when H % 4 == 0: then
+  // thread t moves position t's four values with one 16-byte access through LDS (the per-head
+  // 4-byte accesses touch a line per lane, four times as many L2 requests)
+  __shared__ float s_dt[4][256], s_ddt[4][256];
   const int c = blockIdx.x;
-  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int w = threadIdx.x >> 6;
+  const int h = blockIdx.y * 4 + w;
   const int lane = lane_id();
-  if (h >= d.H) return;
+  if (h >= d.H) return;  // never taken when H % 4 == 0 (every wave of the block then has a head)
   const ChunkInfo ci = chunks[c];
   const int64_t ch = (int64_t)c * d.H + h;
   if (ci.len == 0) {
     if (lane == 0) bf.dA_part[ch] = 0.0f;
     return;
+  }
+  const bool vec_dt = d.a_mode == 0 && d.has_dt && (d.H & 3) == 0 && (reinterpret_cast<uintptr_t>(dt) & 15) == 0;
+  const bool vec_ddt = vec_dt && ddt != nullptr && (reinterpret_cast<uintptr_t>(ddt) & 15) == 0;
+  if (vec_dt) {
+    const int tp = threadIdx.x;  // position; Qpad <= 256 = blockDim.x
+    floatx4 q = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (tp < ci.len) q = *reinterpret_cast<const floatx4*>(dt + (ci.row0 + tp) * (int64_t)d.H + blockIdx.y * 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_dt[e][tp] = q[e];
+    __syncthreads();
   }
   constexpr int per = PER;
   const int64_t base = ch * d.Qpad;
@@ -116,8 +131,9 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
     const float da = v[e] + excl;
     const int64_t row = ci.row0 + l;
     if (d.a_mode == 0) {
-      const float dtv = d.has_dt ? dt[row * d.H + h] : 1.0f;
-      if (ddt && d.has_dt) ddt[row * d.H + h] = t[e] + Ah[h] * da;
+      const float dtv = vec_dt ? s_dt[w][l] : (d.has_dt ? dt[row * d.H + h] : 1.0f);
+      if (vec_ddt) s_ddt[w][l] = t[e] + Ah[h] * da;
+      else if (ddt && d.has_dt) ddt[row * d.H + h] = t[e] + Ah[h] * da;
       dAp += dtv * da;
     } else if (d.a_mode == 1) {
       if (dA_tok) dA_tok[row * d.H + h] = from_f<T>(da);
@@ -125,6 +141,16 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
   }
   for (int o = 32; o > 0; o >>= 1) dAp += __shfl_xor(dAp, o, 64);
   if (lane == 0) bf.dA_part[ch] = dAp;
+  if (vec_ddt) {
+    __syncthreads();
+    const int tp = threadIdx.x;
+    if (tp < ci.len) {
+      floatx4 q;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = s_ddt[e][tp];
+      *reinterpret_cast<floatx4*>(ddt + (ci.row0 + tp) * (int64_t)d.H + blockIdx.y * 4) = q;
+    }
+  }
 }
 
 size_t lds_bwd_col(int dtype, const SsdDims& d) {
