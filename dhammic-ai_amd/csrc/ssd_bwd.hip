@@ -79,33 +79,46 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
   float esum = 0.0f;
   {
     // rowG partial k covers the rows of blocks >= k (column set k of the fused path starts at
-    // column block k); the column / row path writes one partial. A lane's positions share a block.
+    // column block k); the column / row path writes one partial. Rows below 64 k of partial k are
+    // never written, so each position takes partial k only from its own block on: with PER = 3 a
+    // lane's positions can straddle two blocks (lane 21 holds positions 63..65).
+    // Terms (ssd_dA_skip): INTRA = rowG - colG (the segsum of L), CUMSUM = dcs_off (Y_off decay) and
+    // -E + [last] sum E (state-build decay), CHUNK = [last] dtot (the chunk-to-chunk decay).
+    const bool t_intra = !(d.dA_skip & 1), t_cs = !(d.dA_skip & 2);
     float x[PER];
-    ld_per<PER>(bf.rowG + base + l0, x);
-    for (int k = 1; k < bf.nrowg && k <= l0 / 64; ++k) {
-      ld_per<PER>(bf.rowG + k * pstride + base + l0, t);
 #pragma unroll
-      for (int e = 0; e < PER; ++e) x[e] += t[e];
+    for (int e = 0; e < PER; ++e) x[e] = 0.0f;
+    if (t_intra) {
+      ld_per<PER>(bf.rowG + base + l0, x);
+      for (int k = 1; k < bf.nrowg && k <= (l0 + PER - 1) / 64; ++k) {
+        ld_per<PER>(bf.rowG + k * pstride + base + l0, t);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) x[e] += (k <= (l0 + e) / 64) ? t[e] : 0.0f;
+      }
+      ld_per<PER>(bf.colG + base + l0, t);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[e] -= t[e];
     }
-    for (int k = 0; k < bf.ndcs; ++k) {
-      ld_per<PER>(bf.dcs_off + k * pstride + base + l0, t);
+    if (t_cs) {
+      for (int k = 0; k < bf.ndcs; ++k) {
+        ld_per<PER>(bf.dcs_off + k * pstride + base + l0, t);
 #pragma unroll
-      for (int e = 0; e < PER; ++e) x[e] += t[e];
+        for (int e = 0; e < PER; ++e) x[e] += t[e];
+      }
+      ld_per<PER>(bf.eterm + base + l0, t);
     }
-    ld_per<PER>(bf.colG + base + l0, t);
-#pragma unroll
-    for (int e = 0; e < PER; ++e) x[e] -= t[e];
-    ld_per<PER>(bf.eterm + base + l0, t);
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
       const bool ok = l0 + e < ci.len;
-      v[e] = ok ? x[e] - t[e] : 0.0f;
-      esum += ok ? t[e] : 0.0f;
+      const float et = t_cs ? t[e] : 0.0f;
+      v[e] = ok ? x[e] - et : 0.0f;
+      esum += ok ? et : 0.0f;
     }
   }
   for (int o = 32; o > 0; o >>= 1) esum += __shfl_xor(esum, o, 64);
   float dtot = 0.0f;
-  for (int k = 0; k < bf.npass_blk; ++k) dtot += bf.dtot_part[ch * bf.npass_blk + k];
+  if (!(d.dA_skip & 4))
+    for (int k = 0; k < bf.npass_blk; ++k) dtot += bf.dtot_part[ch * bf.npass_blk + k];
   const int last = ci.len - 1;
 #pragma unroll
   for (int e = 0; e < per; ++e)
@@ -135,7 +148,7 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
       if (vec_ddt) s_ddt[w][l] = t[e] + Ah[h] * da;
       else if (ddt && d.has_dt) ddt[row * d.H + h] = t[e] + Ah[h] * da;
       dAp += dtv * da;
-    } else if (d.a_mode == 1) {
+    } else {
       if (dA_tok) dA_tok[row * d.H + h] = from_f<T>(da);
     }
   }

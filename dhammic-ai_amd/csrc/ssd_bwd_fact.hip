@@ -6,33 +6,36 @@
 // Per chunk, head h, 64-token column block j (tokens s) and row blocks i >= j
 // (tokens l), with c_j = cs at the last token of block j:
 //   L[l,s] = exp(cs_l - cs_s) = f_l g_s,   f_l = exp(cs_l - c_j),  g_s = exp(c_j - cs_s)
-//   X'_s   = dt_s g_s x_s,  dY'_l = f_l dy_l          (rows scaled once per head when staged)
+//   v_s    = dt_s g_s,  dY'_l = f_l dy_l,  P[l,s] = dy_l . x_s  (exact: bf16 products, fp32 sums)
 // so with S = C B^T (shared by the heads of a group):
-//   dS[l,s]   += dY'_l . X'_s                 (= dm dt L, summed over heads by the MFMA)
-//   dX_s       = g_s sum_l S[l,s] dY'_l + w_s B_s dst^T,   w_s = exp(clamp(cs_last - cs_s))
-//   G[l,s]     = S[l,s] (dY'_l . X'_s),  rowG_l = sum_s G[l,s],  colG_s = sum_l G[l,s]
+//   dS[l,s]   += f_l v_s P[l,s]               (= dm dt L, summed over the heads)
+//   dX_s       = g_s sum_l S'[l,s] dy_l + w_s B_s dst^T,   S' = f_l S,  w_s = exp(clamp(cs_last - cs_s))
+//   G[l,s]     = S[l,s] f_l v_s P[l,s],  rowG_l = sum_s G[l,s],  colG_s = sum_l G[l,s]
 //   E_s        = pass(cs_last - cs_s) dt_s x_s . (w_s B_s dst^T),  xdx_s = x_s . dX_s
 //   dx_s       = dt_s dX_s + D dy_s
+// G, and with it the decay gradient, is formed in fp32 from fp32 S and the exact
+// products P: the chunk totals of rowG - colG cancel, and the per-head decay
+// gradient (a sum over every token whose terms largely cancel) carries no bf16
+// rounding of S or of row-scaled operands. dX uses raw dy and a bf16 S' per head.
 // The reference clamps every decay exponent to [-20, 20] and masks the clamp's
 // gradient (:192, :230); for a non-increasing cs the factorised form differs
 // only where cs_s - cs_l > 20, by at most e^-20 times the magnitude of the
 // terms. (chunk, head) pairs outside the factorisation's range are flagged by
-// k_chunk_cumsum; here their scaled rows are zero (no dS contribution) and the
+// k_chunk_cumsum; here their factors are zero (no dS contribution) and the
 // exact kernel (k_bwd_main in fixup mode) rewrites their outputs afterwards.
 //
-// One block (8 waves) per (column block j, chunk, group, head slice), heads in
+// One block (12 waves) per (column block j, chunk, group, head slice), heads in
 // sequence. The LDS the block needs allows one block per CU, so its waves are
-// split into two roles that share each SIMD and overlap: waves 0-3 own quadrant
-// (s half w % 2, l half w / 2) of every tile (i, j) for dS and rowG (S^T kept in
-// their registers), waves 4-7 own dX^T tile (p tile (w - 4) / 2, s half w % 2)
-// over all l (S^T read from an LDS copy) and finish the head's tokens. S^T tiles
-// are built once per block. colG_s = X'_s . W_s with
-// W^T = dY'^T S, the same bf16 operands and products as rowG, so the chunk total
-// of rowG - colG cancels as the reference's does. The next head's inputs, and
-// cs / dt at the rows each thread stages and at the token it finishes, are
-// loaded into registers while a head computes; row scales are applied in
-// registers when the head is staged; a head's dx rows and per-token sums go out
-// through LDS while the next head is staged.
+// split into two roles that share each SIMD and overlap: waves 0-7 own quadrant
+// (s half w % 2, l half (w / 2) % 2) of the tiles (j + t, j) with t = w / 4 + 2 u
+// for dS, rowG and colG (S^T of those two tiles kept in fp32 registers, built
+// once per block), waves 8-11 own dX^T tile (p tile (w / 2) % 2, s half w % 2)
+// over all l and finish the head's tokens. While a head is staged the dS waves
+// write its S'^T = f_l S^T tiles to LDS in bf16 from their registers, so every
+// dy row is staged once, unscaled, for both roles. The next head's inputs, and
+// cs / dt at the rows l each dS lane owns and at the token each dX lane
+// finishes, are loaded into registers while a head computes; a head's dx rows
+// and per-token sums go out through LDS while the next head is staged.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
 
@@ -60,48 +63,99 @@ struct BwdFactArgs {
 namespace {
 
 constexpr int kSlots = 4;  // row blocks per column block (Qpad <= 256)
-constexpr int kThreads = 512;
+constexpr int kNsw = 2;    // tiles per dS / rowG wave
+constexpr int kDsWaves = 4 * kSlots / kNsw;   // one quadrant of kNsw tiles each
+constexpr int kSetW = kSlots / kNsw;          // dS waves per quadrant (tile sets)
+constexpr int kThreads = 64 * (kDsWaves + 4);  // + 4 dX waves
 
 template <int PT, int NT>
 struct BwdFactLds {
   static constexpr int PP = 32 * PT, NP = 32 * NT;
   static constexpr int XT = tsize<64, PP>(), SQ = tsize<64, 64>(), DT = tsize<PP, NP>(), BT = tsize<64, NP>();
-  static constexpr int RED = 1024;
-  // bf16: xs, xu, dyu, ot, dYs[4], St[4], dstT, Bt; fp32: reductions
-  static size_t bytes(int) { return 2 * (size_t)(8 * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
+  static constexpr int RED = 1152 + 128 * kSetW + 256;
+  // bf16: xu, ot, dyr[4], St[4], dstT, Bt; fp32: reductions and the v_s row factors
+  static size_t bytes(int) { return 2 * (size_t)((2 + kSlots) * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
 };
 
-template <int PT, int NT>
-struct BwdFactStage {
-  using Rows = TileStage<64, 32 * PT, kThreads>;
-  static constexpr int PER = Rows::PER;  // 16-byte pieces (and rows) per thread of a 64-row tile
-  Rows x, y[kSlots];
-  TileStage<32 * PT, 32 * NT, kThreads> dst;
-  float rcs[kSlots][PER];  // cs at this thread's staged rows of blocks j + t
-  float rdt[PER];          // dt at its staged rows of block j (as loaded: 0 where absent)
-  float ecs, edt;          // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
-  float cj, cl;            // cs at the last token of block j and of the chunk
-  float D;                 // the head's D (0 without D)
-  int fast;
+// One register array serves both roles (roles are fixed per wave): a dS wave keeps the S^T and
+// dS quadrants of its kNsw tiles in it (entries 4 u .. 4 u + 3 and 4 (kNsw + u) .. + 3), a dX wave
+// the next head's tiles, loaded while the current head computes and staged to LDS by the 4 dX
+// waves (x rows, dy rows of the kSlots row blocks, dst). Carried through the head loop as one
+// array, it costs the registers of the larger use instead of both.
+constexpr int kUR = 8 * kNsw;
+constexpr int kXThr = 256;  // dX-wave threads that stage a head
+
+template <int ROWS, int W>
+struct XTile {
+  static constexpr int NVEC = ROWS * W / 8;
+  static constexpr int PER = (NVEC + kXThr - 1) / kXThr;
 };
 
-// Row-major staged 64-row tile to LDS, the piece of pass q scaled by sc[q] (fp32) before rounding.
-template <int W, int NTHR>
-__device__ __forceinline__ void tstage_store_sc(const TileStage<64, W, NTHR>& s, bf16* t,
-                                                const float (&sc)[TileStage<64, W, NTHR>::PER]) {
+// Tile rows [0, nrows) and columns [0, width) of a row-major bf16 tensor at g into R[0 .. PER);
+// zeros elsewhere (buffer range check). xt: this thread's index among the staging threads. Every
+// piece is loaded unconditionally (a masked piece reads zeros), so each register is always
+// written by its load and the compiler needs no copy that would wait for the load.
+template <int ROWS, int W>
+__device__ __forceinline__ void xt_load(u32x4* R, int xt, const bf16* __restrict__ g, int64_t ld, int nrows,
+                                        int width) {
+  constexpr int CPR = W / 8;
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g);
+#pragma unroll
+  for (int q = 0; q < XTile<ROWS, W>::PER; ++q) {
+    const int id = xt + q * kXThr;
+    const int r = id / CPR, k = (id % CPR) * 8;
+    const bool ok = (XTile<ROWS, W>::NVEC % kXThr == 0 || id < XTile<ROWS, W>::NVEC) && r < nrows && k < width;
+    R[q] = __builtin_bit_cast(u32x4, buf_ld16(rs, (int)(((int64_t)r * ld + k) * 2), ok));
+  }
+}
+template <int ROWS, int W>
+__device__ __forceinline__ void xt_store(const u32x4* R, int xt, bf16* t) {
   constexpr int CPR = W / 8;
 #pragma unroll
-  for (int q = 0; q < TileStage<64, W, NTHR>::PER; ++q) {
-    const int id = threadIdx.x + q * NTHR;
-    if (TileStage<64, W, NTHR>::NVEC % NTHR == 0 || id < TileStage<64, W, NTHR>::NVEC) {
+  for (int q = 0; q < XTile<ROWS, W>::PER; ++q) {
+    const int id = xt + q * kXThr;
+    if (XTile<ROWS, W>::NVEC % kXThr == 0 || id < XTile<ROWS, W>::NVEC) {
       const int r = id / CPR, k = (id % CPR) * 8;
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * sc[q]);
-      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = o;
+      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = __builtin_bit_cast(bf16x8, R[q]);
     }
   }
 }
+__device__ __forceinline__ floatx16 ur_get(const u32x4* R) {
+  floatx16 f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[4 * q + e] = __uint_as_float(R[q][e]);
+  return f;
+}
+__device__ __forceinline__ void ur_set(u32x4* R, const floatx16& f) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) R[q][e] = __float_as_uint(f[4 * q + e]);
+}
+
+// Eight bf16 values times eight fp32 factors f[0..7] (16-byte aligned in LDS), rounded to bf16.
+__device__ __forceinline__ bf16x8 scale8(const bf16x8 v, const float* f) {
+  const floatx4 a = *reinterpret_cast<const floatx4*>(f);
+  const floatx4 b = *reinterpret_cast<const floatx4*>(f + 4);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    o[e] = (bf16)((float)v[e] * a[e]);
+    o[e + 4] = (bf16)((float)v[e + 4] * b[e]);
+  }
+  return o;
+}
+
+// Per-head scalars loaded with the next head's tiles (dX waves).
+struct BwdFactScalars {
+  float fcs;        // cs at row 64 j + (staging thread index): the head's f_l
+  float ecs, edt;   // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
+  float cj, cl;     // cs at the last token of block j and of the chunk
+  float D;          // the head's D (0 without D)
+  int fast;
+};
 
 }  // namespace
 
@@ -117,10 +171,10 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   const int U = d.max_chunks * d.G * a.nslices;
   const int U8 = (U + 7) / 8 * 8;
   const int j = blockIdx.x / U8;
-  const int u = blockIdx.x % U8;
-  if (u >= U) return;
-  const int c = u % d.max_chunks;
-  const int gsl = u / d.max_chunks;
+  const int ub = blockIdx.x % U8;
+  if (ub >= U) return;
+  const int c = ub % d.max_chunks;
+  const int gsl = ub / d.max_chunks;
   const int g = gsl / a.nslices, slc = gsl % a.nslices;
   const ChunkInfo ci = a.chunks[c];
   const int nbl = (ci.len + 63) >> 6;
@@ -131,29 +185,31 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   if (h_lo >= h_hi) return;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool xrole = w >= 4;                    // dX / token waves (else dS / rowG waves)
+  const bool xrole = w >= kDsWaves;             // dX / token waves (else dS / rowG waves)
   const int wr = w & 1, wc = (w >> 1) & 1;      // dS / rowG quadrant: s half, l half
+  const int ws = (w >> 2) % kSetW;              // dS / rowG tiles t = ws + kSetW u
   const int pt = (w >> 1) & 1, sr = w & 1;      // dX^T tile: p tile, s half
   int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
   const int Qpad = d.Qpad;
   const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
 
-  bf16* xs = reinterpret_cast<bf16*>(smem);  // X' rows of block j      [64][PP]
-  bf16* xu = xs + XT;                        // x rows of block j       [64][PP]
-  bf16* dyu = xu + XT;                       // dy rows of block j      [64][PP]
-  bf16* ot = dyu + XT;                       // dx rows of block j      [64][PP]
-  bf16* dYs = ot + XT;                       // dY' rows of blocks i    [4][64][PP]
-  bf16* St = dYs + kSlots * XT;              // S^T tiles (i, j)        [4][64 s][64 l]
-  bf16* dstT = St + kSlots * SQ;             // dst                     [PP][NP]
-  bf16* Bt = dstT + LD::DT;                  // B rows of block j       [64][NP]
+  bf16* xu = reinterpret_cast<bf16*>(smem);  // x rows of block j          [64][PP]
+  bf16* ot = xu + XT;                        // dx rows of block j         [64][PP]
+  bf16* dyr = ot + XT;                       // dy rows of blocks j + t    [4][64][PP] (slot 0: block j)
+  bf16* St = dyr + kSlots * XT;              // S'^T tiles (j + t, j)      [4][64 s][64 l], per head
+  bf16* dstT = St + kSlots * SQ;             // dst                        [PP][NP]
+  bf16* Bt = dstT + LD::DT;                  // B rows of block j          [64][NP]
   float* red = reinterpret_cast<float*>(Bt + LD::BT);
-  float* red_row = red;        // [4 slots][2 wr][64]
-  float* red_col = red + 512;  // [2 pt][64]
-  float* red_e = red + 640;    // [2 pt][64]
-  float* red_x = red + 768;    // [2 pt][64]
-  float* red_d = red + 896;    // [4 dX waves]
+  float* red_e = red;           // [2 pt][64]
+  float* red_x = red + 128;     // [2 pt][64]
+  float* red_d = red + 256;     // [4 dX waves]
+  float* vrow = red + 320;      // [64] v_s = dt_s g_s of the current head (0 for a flagged head)
+  float* red_row = red + 384;   // [4 slots][2 wr][64]
+  float* red_col = red + 896;   // [kSetW][2 wc][64]
+  float* frow = red_col + 128 * kSetW;  // [256] f_l = exp(cs_l - c_j) at rows 64 j + l of the current head
 
-  // ---- B rows of block j; S^T tiles (i, j): rows s (block j), columns l (block i) ----
+  // ---- B rows of block j; the dS waves' S^T quadrants of tiles (j + t, j), t = ws + kSetW u: rows s
+  // (block j), columns l (block j + t), kept in fp32 registers for every head ----
   {
     TileStage<64, NP, kThreads> st;
     tstage_load_v(st, a.Bm + (int64_t)(ci.row0 + 64 * j) * brow + (int64_t)g * d.N, brow,
@@ -161,78 +217,80 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     tstage_store(st, Bt);
   }
   __syncthreads();
+  u32x4 UR[kUR];
 #pragma unroll
-  for (int t = 0; t < kSlots; ++t) {
-    floatx16 sacc;
-    zero(sacc);
-    const int i = j + t;
-    if (!xrole && t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
-      const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
-      const int lrow = 64 * i + 32 * wc + l32;
-      bf16x8 cb[NP / 16];
+  for (int q = 0; q < kUR; ++q) UR[q] = u32x4{0u, 0u, 0u, 0u};
+  if (!xrole) {
 #pragma unroll
-      for (int kk = 0; kk < NP / 16; ++kk) {
-        const int n0 = 16 * kk + 8 * hh;
-        cb[kk] = buf_ld16(rc, (int)(((int64_t)lrow * brow + n0) * 2), lrow < ci.len && n0 < d.N);
+    for (int uu = 0; uu < kNsw; ++uu) {
+      const int t = ws + kSetW * uu, i = j + t;
+      floatx16 Sq;
+      zero(Sq);
+      if (t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
+        const __amdgpu_buffer_rsrc_t rc = buf_rsrc(a.Cm + (int64_t)ci.row0 * brow + (int64_t)g * d.N);
+        const int lrow = 64 * i + 32 * wc + l32;
+        bf16x8 cb[NP / 16];
+#pragma unroll
+        for (int kk = 0; kk < NP / 16; ++kk) {
+          const int n0 = 16 * kk + 8 * hh;
+          cb[kk] = buf_ld16(rc, (int)(((int64_t)lrow * brow + n0) * 2), lrow < ci.len && n0 < d.N);
+        }
+#pragma unroll
+        for (int kk = 0; kk < NP / 16; ++kk) mfma(Sq, tld8<NP>(Bt, 32 * wr + l32, 16 * kk + 8 * hh), cb[kk]);
+        if (t == 0) {  // diagonal tile: s > l is outside the causal mask
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if (32 * wr + acc_row(v, lane) > 32 * wc + l32) Sq[v] = 0.0f;
+        }
       }
+      ur_set(UR + 4 * uu, Sq);  // dS (entries 4 (kNsw + u) ..) starts at zero
+      // bf16 copy of S^T[s][l] for the dX waves (also for tiles and quadrants that stay zero)
+      if (t < kSlots) {
 #pragma unroll
-      for (int kk = 0; kk < NP / 16; ++kk) mfma(sacc, tld8<NP>(Bt, 32 * wr + l32, 16 * kk + 8 * hh), cb[kk]);
-      if (t == 0) {  // diagonal tile: s > l is outside the causal mask
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (32 * wr + acc_row(v, lane) > 32 * wc + l32) sacc[v] = 0.0f;
+        for (int v = 0; v < 16; ++v) St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)Sq[v];
       }
-    }
-    // S^T[s][l] of the quadrant to LDS (also for tiles / quadrants that stay zero)
-    if (!xrole) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)sacc[v];
     }
   }
 
-  floatx16 dS[kSlots];
-#pragma unroll
-  for (int t = 0; t < kSlots; ++t) zero(dS[t]);
-
-  using HS = BwdFactStage<PT, NT>;
-  constexpr int PER = HS::PER, RPP = kThreads / (PP / 8);  // rows of a staged tile per pass
-  HS hs;
-  const int r0 = min((int)threadIdx.x / (PP / 8), 63);    // first staged row of this thread
-  const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);  // token this lane finishes
+  // dX-wave tile pieces in UR: x rows, dy rows of row block j + t, dst
+  using TX = XTile<64, PP>;
+  using TD = XTile<PP, NP>;
+  constexpr int oX = 0, oY = TX::PER, oD = TX::PER * (1 + kSlots);
+  static_assert(oD + TD::PER <= kUR, "dX staging registers");
+  BwdFactScalars hs{};  // loaded by the dX waves; zero (unused) in the dS waves
+  const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);  // token this lane finishes (dX waves)
   // dt as used: the loaded value where the token exists and dt is given, else 1
   auto dt_use = [&](float v, int tok) { return (d.has_dt && tok < ci.len) ? v : 1.0f; };
-  // All per-head loads are issued unconditionally (masked buffer loads read zeros) and
-  // used only after the staging barrier, so the compiler's wait for them stays there
-  // instead of draining the whole prefetch right after it is issued.
+  // The next head's loads, issued by the dX waves only (the dS waves read what they need of a head
+  // from LDS and issue no global load in the head loop, so no load of theirs is ever pending where
+  // the dX waves reuse registers). All are unconditional masked buffer loads used only after the
+  // staging barrier, and every per-lane offset derives from an opaque thread id recomputed per head
+  // (held across the head loop, these offsets spill, and their reloads wait for the prefetch).
   auto load_head = [&](int h) {
-    const int64_t xo = (int64_t)h * d.P;
-    tstage_load_v(hs.x, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
-#pragma unroll
-    for (int t = 0; t < kSlots; ++t)
-      if (t < nt_i)
-        tstage_load_v(hs.y[t], a.dy + (int64_t)(ci.row0 + 64 * (j + t)) * xrow + xo, xrow,
-                      min(64, ci.len - 64 * (j + t)), d.P);
-    tstage_load_v(hs.dst, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     const float* csh = a.cs + ((int64_t)c * d.H + h) * Qpad;
     const __amdgpu_buffer_rsrc_t rcs = buf_rsrc(csh);
+    const int xt = tid - 64 * kDsWaves;
+    const int tok = 64 * j + 32 * (w & 1) + (tid & 31);
     const __amdgpu_buffer_rsrc_t rdt = buf_rsrc(d.has_dt ? a.dt + (int64_t)ci.row0 * d.H + h : csh);
+    hs.fcs = buf_ldf(rcs, (64 * j + xt) * 4, 64 * j + xt < Qpad);
+    hs.ecs = buf_ldf(rcs, tok * 4, true);
+    hs.edt = buf_ldf(rdt, tok * d.H * 4, d.has_dt && tok < ci.len);
+    hs.cl = buf_ldf(rcs, (Qpad - 1) * 4, true);
+    hs.D = buf_ldf(buf_rsrc(d.has_D ? a.Dv : csh), h * 4, d.has_D);
+    hs.cj = buf_ldf(rcs, (64 * j + 63) * 4, true);
+    hs.fast = __float_as_int(buf_ldf(buf_rsrc(a.fast + (int64_t)c * d.H), h * 4, true));
+    const int64_t xo = (int64_t)h * d.P;
+    xt_load<64, PP>(UR + oX, xt, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
 #pragma unroll
-    for (int t = 0; t < kSlots; ++t)
-#pragma unroll
-      for (int q = 0; q < PER; ++q)
-        hs.rcs[t][q] = buf_ldf(rcs, (64 * (j + t) + min(r0 + RPP * q, 63)) * 4, t < nt_i);
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int tok = 64 * j + min(r0 + RPP * q, 63);
-      hs.rdt[q] = buf_ldf(rdt, tok * d.H * 4, d.has_dt && tok < ci.len);
+    for (int t = 0; t < kSlots; ++t) {
+      // row blocks past the chunk read zeros (from the chunk's first row, so the base stays inside dy)
+      const bool tv = t < nt_i;
+      xt_load<64, PP>(UR + oY + TX::PER * t, xt, a.dy + (int64_t)(ci.row0 + (tv ? 64 * (j + t) : 0)) * xrow + xo,
+                      xrow, tv ? min(64, ci.len - 64 * (j + t)) : 0, d.P);
     }
-    hs.ecs = buf_ldf(rcs, te * 4, true);
-    hs.edt = buf_ldf(rdt, te * d.H * 4, d.has_dt && te < ci.len);
-    hs.cj = csh[64 * j + 63];
-    hs.cl = csh[Qpad - 1];
-    hs.fast = a.fast[(int64_t)c * d.H + h];
-    hs.D = d.has_D ? a.Dv[h] : 0.0f;
+    xt_load<PP, NP>(UR + oD, xt, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
   };
   // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
   auto flush = [&](int h) {
@@ -240,7 +298,10 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     if (threadIdx.x < 64) {
       const int tl = threadIdx.x, tg = 64 * j + tl;
       if (tg < ci.len) {
-        a.colG[hq + tg] = red_col[tl] + red_col[64 + tl];
+        float cg = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 2 * kSetW; ++q) cg += red_col[64 * q + tl];
+        a.colG[hq + tg] = cg;
         a.eterm[hq + tg] = red_e[tl] + red_e[64 + tl];
         a.xdx[hq + tg] = red_x[tl] + red_x[64 + tl];
       }
@@ -267,7 +328,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   // token rows at any moment instead of all the same one (HBM channel spread)
   const int nh = h_hi - h_lo, hrot = c % nh;
   auto head = [&](int k) { const int m = k + hrot; return h_lo + (m >= nh ? m - nh : m); };
-  load_head(head(0));
+  if (xrole) load_head(head(0));
   for (int k = 0; k < nh; ++k) {
     lane = opaque_lane();
     hh = lane >> 5;
@@ -275,129 +336,129 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     // previous head: LDS reads done, reductions and ot complete (LDS only: the previous
     // head's global stores and this head's prefetch stay in flight)
     lds_barrier();
-    // row scales (zero for a flagged head): X' rows dt_s exp(c_j - cs_s), dY' rows exp(cs_l - c_j)
-    {
-      const bool ok = hs.fast != 0;
-      const float cj2 = hs.cj * SSD_LOG2E;
-      float sc[PER];
-#pragma unroll
-      for (int q = 0; q < PER; ++q)
-        sc[q] = ok ? dt_use(hs.rdt[q], 64 * j + min(r0 + RPP * q, 63)) * exp2_fast(cj2 - hs.rcs[0][q] * SSD_LOG2E)
-                   : 0.0f;
-      tstage_store_sc(hs.x, xs, sc);
-#pragma unroll
-      for (int t = 0; t < kSlots; ++t)
-        if (t < nt_i) {
-#pragma unroll
-          for (int q = 0; q < PER; ++q) sc[q] = ok ? exp2_fast(hs.rcs[t][q] * SSD_LOG2E - cj2) : 0.0f;
-          tstage_store_sc(hs.y[t], dYs + t * XT, sc);
-        }
-    }
-    tstage_store(hs.x, xu);
-    tstage_store(hs.y[0], dyu);
-    tstage_store(hs.dst, dstT);
     // this head's per-token values for the finishing step (hs is reloaded below)
+    const bool ok = hs.fast != 0;
     const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = dt_use(hs.edt, te);
     const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
     const float Dh = hs.D;
+    if (xrole) {
+      int tid = threadIdx.x;
+      asm volatile("" : "+v"(tid));
+      const int xt = tid - 64 * kDsWaves;
+      xt_store<64, PP>(UR + oX, xt, xu);
+#pragma unroll
+      for (int t = 0; t < kSlots; ++t)
+        if (t < nt_i) xt_store<64, PP>(UR + oY + TX::PER * t, xt, dyr + t * XT);
+      xt_store<PP, NP>(UR + oD, xt, dstT);
+      // f_l of rows 64 j + xt and v_s of the head's tokens s (block j); zero for a flagged head
+      frow[xt] = (ok && xt < 64 * nt_i) ? exp2_fast(hs.fcs * SSD_LOG2E - e_cj2) : 0.0f;
+      if (pt == 0 && hh == 0) vrow[32 * sr + l32] = ok ? e_dt * exp2_fast(e_cj2 - e_c2) : 0.0f;
+    }
     if (k > 0) flush(head(k - 1));  // its LDS (ot, reductions) is not touched by the staging above
     lds_barrier();
-    if (k + 1 < nh) load_head(head(k + 1));
 
     if (!xrole) {
-      // ---- tiles (i, j): X' dY'^T (quadrant) into dS, rowG from S * (X' dY'^T) ----
+      // ---- tiles (j + t, j): P = x dy^T (quadrant, exact), then in fp32
+      // dS += f_l v_s P, G = S f_l v_s P, rowG (over s: registers), colG (over l: across lanes) ----
+      float vs[16];
+      rows16(vrow + 32 * wr, vs);
+      float colp = 0.0f;  // colG of row s = 32 wr + acc_row((lane >> 1) & 15, lane) over this wave's tiles
 #pragma unroll
-      for (int t = 0; t < kSlots; ++t) {
+      for (int uu = 0; uu < kNsw; ++uu) {
+        const int t = ws + kSetW * uu;
         if (t >= nt_i) continue;
-        const bf16* dyt = dYs + t * XT;
         if (!(t == 0 && wr == 1 && wc == 0)) {
-          floatx16 tq;
-          zero(tq);
+          const bf16* dyt = dyr + t * XT;
+          floatx16 P;
+          zero(P);
 #pragma unroll
           for (int kk = 0; kk < PP / 16; ++kk)
-            mfma(tq, tld8<PP>(xs, 32 * wr + l32, 16 * kk + 8 * hh), tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh));
-          // this head's X' dY'^T: into the head-summed dS, and G over the quadrant
-#pragma unroll
-          for (int v = 0; v < 16; ++v) dS[t][v] += tq[v];
-          // G over the quadrant: lane l holds column l, registers the s rows (S^T read back
-          // from LDS in that layout, four rows per transposed read)
+            mfma(P, tld8<PP>(xu, 32 * wr + l32, 16 * kk + 8 * hh), tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh));
+          const float fl = frow[64 * t + 32 * wc + l32];
+          const floatx16 Sq = ur_get(UR + 4 * uu);
+          floatx16 dSq = ur_get(UR + 4 * (kNsw + uu));
+          float G[16];
           float rs = 0.0f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const bf16x4 sv = ttr4<64>(St + t * SQ, 32 * wr + 8 * r + 4 * hh, 32 * wc + 16 * ((lane >> 4) & 1), lane);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rs = fmaf((float)sv[e], tq[4 * r + e], rs);
+          for (int v = 0; v < 16; ++v) {
+            const float q = P[v] * (vs[v] * fl);
+            dSq[v] += q;
+            G[v] = Sq[v] * q;
+            rs += G[v];
           }
+          ur_set(UR + 4 * (kNsw + uu), dSq);
           rs = add_xor32(rs);
           if (hh == 0) red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
+          colp += half_reduce16(G, lane);
         } else if (hh == 0) {
           red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
         }
       }
-    } else if (pt >= PT) {
-      // dX waves past the p tiles add zeros
-      if (hh == 0) {
-        red_e[pt * 64 + 32 * sr + l32] = 0.0f;
-        red_x[pt * 64 + 32 * sr + l32] = 0.0f;
-        red_col[pt * 64 + 32 * sr + l32] = 0.0f;
-      }
-      if (lane == 0) red_d[w - 4] = 0.0f;
+      if ((l32 & 1) == 0) red_col[(ws * 2 + wc) * 64 + 32 * wr + acc_row((l32 >> 1) & 15, lane)] = colp;
     } else {
-      // ---- dX^T += dY'^T S over the tiles (i, j); state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
-      floatx16 dXa, dXs;
-      zero(dXa);
-      zero(dXs);
-#pragma unroll
-      for (int t = 0; t < kSlots; ++t) {
-        if (t >= nt_i) continue;
-        const bf16* dyt = dYs + t * XT;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh));
-      }
-#pragma unroll
-      for (int kk = 0; kk < NP / 16; ++kk)
-        mfma(dXs, tld8<NP>(dstT, 32 * pt + l32, 16 * kk + 8 * hh), tld8<NP>(Bt, 32 * sr + l32, 16 * kk + 8 * hh));
-
-      // ---- per token s (lane) of block j: scale, sums, dx ----
-      const int s_loc = 32 * sr + l32, sg = 64 * j + s_loc;
-      const float gs = exp2_fast(e_cj2 - e_c2);
-      const float dw = e_cl2 - e_c2;
-      const float ws = sg < ci.len ? exp2_fast(clamp_med3(dw, -SSD_T2, SSD_T2)) : 0.0f;
-      const float pw = fabsf(dw) < SSD_T2 ? 1.0f : 0.0f;
-      const float dts = e_dt;
-      float esum = 0.0f, xsum = 0.0f, dsum = 0.0f, csum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int p0 = 32 * pt + 8 * r + 4 * hh;
-        const bf16x4 xv = tld4<PP>(xu, s_loc, p0);
-        const bf16x4 yv = tld4<PP>(dyu, s_loc, p0);
-        const bf16x4 sv = tld4<PP>(xs, s_loc, p0);
-        bf16x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * r + e;
-          const float xf = (float)xv[e], yf = (float)yv[e];
-          const float di = gs * dXa[v], ds = ws * dXs[v];
-          const float dX = di + ds;
-          csum = fmaf((float)sv[e], dXa[v], csum);
-          esum = fmaf(xf, ds, esum);
-          xsum = fmaf(xf, dX, xsum);
-          dsum = fmaf(xf, yf, dsum);
-          o[e] = (bf16)fmaf(dts, dX, Dh * yf);
+      if (k + 1 < nh) load_head(head(k + 1));
+      if (pt >= PT) {
+        // dX waves past the p tiles add zeros
+        if (hh == 0) {
+          red_e[pt * 64 + 32 * sr + l32] = 0.0f;
+          red_x[pt * 64 + 32 * sr + l32] = 0.0f;
         }
-        *reinterpret_cast<bf16x4*>(ot + toff<PP>(s_loc, p0)) = o;
+        if (lane == 0) red_d[w - kDsWaves] = 0.0f;
+      } else {
+        // ---- dX^T += dy^T S' over the tiles (j + t, j), S'[l][s] = f_l S[l][s] scaled in registers;
+        // state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
+        floatx16 dXa, dXs;
+        zero(dXa);
+        zero(dXs);
+#pragma unroll
+        for (int t = 0; t < kSlots; ++t) {
+          if (t >= nt_i) continue;
+          const bf16* dyt = dyr + t * XT;
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+            mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane),
+                 scale8(tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh), frow + 64 * t + 16 * kk + 8 * hh));
+        }
+#pragma unroll
+        for (int kk = 0; kk < NP / 16; ++kk)
+          mfma(dXs, tld8<NP>(dstT, 32 * pt + l32, 16 * kk + 8 * hh), tld8<NP>(Bt, 32 * sr + l32, 16 * kk + 8 * hh));
+
+        // ---- per token s (lane) of block j: scale, sums, dx ----
+        const int s_loc = 32 * sr + l32, sg = 64 * j + s_loc;
+        const float gs = exp2_fast(e_cj2 - e_c2);
+        const float dw = e_cl2 - e_c2;
+        const float wsd = sg < ci.len ? exp2_fast(clamp_med3(dw, -SSD_T2, SSD_T2)) : 0.0f;
+        const float pw = fabsf(dw) < SSD_T2 ? 1.0f : 0.0f;
+        const float dts = e_dt;
+        float esum = 0.0f, xsum = 0.0f, dsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p0 = 32 * pt + 8 * r + 4 * hh;
+          const bf16x4 xv = tld4<PP>(xu, s_loc, p0);
+          const bf16x4 yv = tld4<PP>(dyr, s_loc, p0);
+          bf16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * r + e;
+            const float xf = (float)xv[e], yf = (float)yv[e];
+            const float di = gs * dXa[v], ds = wsd * dXs[v];
+            const float dX = di + ds;
+            esum = fmaf(xf, ds, esum);
+            xsum = fmaf(xf, dX, xsum);
+            dsum = fmaf(xf, yf, dsum);
+            o[e] = (bf16)fmaf(dts, dX, Dh * yf);
+          }
+          *reinterpret_cast<bf16x4*>(ot + toff<PP>(s_loc, p0)) = o;
+        }
+        esum = add_xor32(esum);
+        xsum = add_xor32(xsum);
+        dsum = wave_sum(dsum);
+        if (hh == 0) {
+          red_e[pt * 64 + s_loc] = esum * dts * pw;
+          red_x[pt * 64 + s_loc] = xsum;
+        }
+        if (lane == 0) red_d[w - kDsWaves] = dsum;
       }
-      esum = add_xor32(esum);
-      xsum = add_xor32(xsum);
-      csum = add_xor32(csum);
-      dsum = wave_sum(dsum);
-      if (hh == 0) {
-        red_e[pt * 64 + s_loc] = esum * dts * pw;
-        red_x[pt * 64 + s_loc] = xsum;
-        red_col[pt * 64 + s_loc] = csum;
-      }
-      if (lane == 0) red_d[w - 4] = dsum;
     }
   }
   __syncthreads();
@@ -407,7 +468,8 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   if (xrole) return;
   float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
 #pragma unroll
-  for (int t = 0; t < kSlots; ++t) {
+  for (int uu = 0; uu < kNsw; ++uu) {
+    const int t = ws + kSetW * uu;
     if (t >= nt_i) continue;
     float* tile = dSbase + (int64_t)((j + t) * nb + j) * 4096;
     const int l_loc = 32 * wc + l32;
@@ -417,7 +479,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int s_loc = 32 * wr + 8 * r + 4 * hh + e;
-        q[e] = (t == 0 && s_loc > l_loc) ? 0.0f : dS[t][4 * r + e];
+        q[e] = (t == 0 && s_loc > l_loc) ? 0.0f : __uint_as_float(UR[4 * (kNsw + uu) + r][e]);
       }
       *reinterpret_cast<floatx4*>(tile + l_loc * 64 + 32 * wr + 8 * r + 4 * hh) = q;
     }

@@ -45,6 +45,9 @@ int plan(const ssd_desc_t* s, Plan* p) {
   if (s->varlen && (s->batch != 1 || s->nseq < 1)) return SSD_ERR_INVALID;
   if ((s->a_mode == SSD_A_CUMSUM || s->want_A_cumsum) && (s->varlen || s->seqlen % s->chunk)) return SSD_ERR_INVALID;
   if (s->has_z && !(s->norm_eps >= 0.0f)) return SSD_ERR_INVALID;
+  if (s->dA_skip & ~(SSD_DA_SKIP_INTRA | SSD_DA_SKIP_CUMSUM | SSD_DA_SKIP_CHUNK)) return SSD_ERR_INVALID;
+  // a cached A_cumsum carries no gradient, and neither does the decay_chunk built from it
+  if (s->a_mode == SSD_A_CUMSUM && (~s->dA_skip & (SSD_DA_SKIP_CUMSUM | SSD_DA_SKIP_CHUNK))) return SSD_ERR_INVALID;
   if (s->chunk > SSD_MAX_CHUNK || s->headdim > SSD_MAX_HEADDIM || s->dstate > SSD_MAX_DSTATE)
     return SSD_ERR_UNSUPPORTED;
   if (s->varlen && s->nseq > kMaxSeq) return SSD_ERR_UNSUPPORTED;
@@ -67,6 +70,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   d.a_mode = s->a_mode; d.has_dt = s->has_dt != 0; d.has_D = s->has_D != 0; d.has_z = s->has_z != 0;
   d.has_init = s->has_init != 0; d.has_dfinal = s->has_dfinal != 0; d.varlen = s->varlen != 0;
   d.eps = s->norm_eps;
+  d.dA_skip = s->dA_skip;
   p->dtype = s->dtype;
   p->state_dtype = s->state_dtype;
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
@@ -337,7 +341,11 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   }
   SSD_PHASE(tm, SSD_PH_BWD_FINISH,
             launch_bwd_finish(p.dtype, d, b, in, d.has_dt ? a->ddt : nullptr,
-                              d.a_mode == SSD_A_PER_TOKEN ? a->dA : nullptr, s));
+                              (d.a_mode == SSD_A_PER_TOKEN ||
+                               (d.a_mode == SSD_A_CUMSUM && !(d.dA_skip & SSD_DA_SKIP_INTRA)))
+                                  ? a->dA
+                                  : nullptr,
+                              s));
   if (p.nslices > 1 && !fused) {
     const int64_t nelem = d.R * d.G * d.N;
     SSD_TRY(tm.begin(SSD_PH_BWD_REDUCE_BC));
@@ -385,6 +393,6 @@ const char* ssd_status_string(int status) {
   }
 }
 
-int ssd_abi_version(void) { return 1; }
+int ssd_abi_version(void) { return 2; }
 
 }  // extern "C"

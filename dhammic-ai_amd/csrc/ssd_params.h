@@ -14,6 +14,7 @@ struct SsdDims {
   int64_t R;                         // rows of the packed token axis (batch * seqlen)
   int a_mode, has_dt, has_D, has_z, has_init, has_dfinal, varlen;
   float eps;
+  int dA_skip;                       // enum ssd_dA_skip bits (terms left out of the decay gradient)
   // 16-byte global loads allowed for x/dy/z-shaped tensors and for B/C (set per call
   // from the feature widths and the pointers' alignment)
   bool vec_x, vec_bc;

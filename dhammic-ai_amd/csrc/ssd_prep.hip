@@ -131,10 +131,18 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
     for (int e = 1; e < per; ++e) ok = ok && v[e] <= v[e - 1];
     const float prev = __shfl_up(v[per - 1], 1, 64);
     if (lane > 0) ok = ok && v[0] <= prev;
-    const int lpb = 64 / per;  // lanes per 64-token block
-    const int first = lane & ~(lpb - 1);
-    const float top = __shfl(v[0], first, 64), bot = __shfl(v[per - 1], first + lpb - 1, 64);
-    ok = ok && (top - bot) <= SSD_FACT_RANGE;
+    // Lane j < Qpad / 64 checks block j from its exact end positions 64 j and 64 j + 63, fetched
+    // from the lanes and elements that own them (with per = 3 a block does not start on a lane).
+    const int jb = lane < per ? lane : 0;
+    const int ptop = 64 * jb, pbot = 64 * jb + 63;
+    float top = 0.0f, bot = 0.0f;
+    for (int e = 0; e < per; ++e) {
+      const float a1 = __shfl(v[e], ptop / per, 64);
+      const float a2 = __shfl(v[e], pbot / per, 64);
+      if (e == ptop % per) top = a1;
+      if (e == pbot % per) bot = a2;
+    }
+    if (lane < per) ok = ok && (top - bot) <= SSD_FACT_RANGE;
     const bool all_ok = __all(ok);
     if (lane == 0) fast[(int64_t)c * d.H + h] = all_ok ? 1 : 0;
   }

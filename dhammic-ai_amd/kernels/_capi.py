@@ -27,6 +27,11 @@ SSD_A_PER_HEAD = 0
 SSD_A_PER_TOKEN = 1
 SSD_A_CUMSUM = 2
 
+# enum ssd_dA_skip
+SSD_DA_SKIP_INTRA = 1
+SSD_DA_SKIP_CUMSUM = 2
+SSD_DA_SKIP_CHUNK = 4
+
 # enum ssd_phase (launch order of ssd_fwd / ssd_bwd)
 PHASES = ("chunk_table", "cumsum", "fwd_state", "fwd_pass", "fwd_scan", "norm_fwd", "norm_bwd", "norm_dw",
           "bwd_state", "bwd_pass", "bwd_col", "bwd_row", "bwd_finish", "bwd_reduce_bc", "bwd_reduce_heads")
@@ -36,7 +41,7 @@ SSD_WS_SAVED = 0
 SSD_WS_FWD_SCRATCH = 1
 SSD_WS_BWD_SCRATCH = 2
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -50,7 +55,7 @@ class SsdDesc(ctypes.Structure):
         ("dtype", _i32), ("state_dtype", _i32), ("a_mode", _i32),
         ("has_dt", _i32), ("has_D", _i32), ("has_z", _i32), ("has_init", _i32),
         ("has_dfinal", _i32), ("varlen", _i32), ("want_final", _i32), ("want_A_cumsum", _i32),
-        ("norm_eps", ctypes.c_float),
+        ("norm_eps", ctypes.c_float), ("dA_skip", _i32),
     ]
 
 

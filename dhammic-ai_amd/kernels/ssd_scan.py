@@ -62,6 +62,7 @@ class _Cfg:
     state_code: int
     want_acs: bool
     eps: float
+    dA_skip: int = 0
 
 
 def _desc(cfg: _Cfg, x, B, dt, D, z, init, has_dfinal=False):
@@ -81,6 +82,7 @@ def _desc(cfg: _Cfg, x, B, dt, D, z, init, has_dfinal=False):
     d.want_final = 1
     d.want_A_cumsum = int(cfg.want_acs)
     d.norm_eps = cfg.eps
+    d.dA_skip = cfg.dA_skip
     return d
 
 
@@ -119,8 +121,20 @@ def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None):
     return y, final, acs, saved
 
 
+def _dA_out(cfg: _Cfg, x, A):
+    """The log-decay gradient buffer ssd_bwd writes, or None: A's own shape for a per-head or
+    per-token A; with a cached A_cumsum, the per-token shape (b, T, H) when the intra-chunk term
+    (the reference's L built from A) is not cached too."""
+    if cfg.a_mode in (C_.SSD_A_PER_HEAD, C_.SSD_A_PER_TOKEN):
+        return torch.empty_like(A)
+    if not cfg.dA_skip & C_.SSD_DA_SKIP_INTRA:
+        return torch.empty(x.shape[:3], dtype=x.dtype, device=x.device)
+    return None
+
+
 def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal, events=None):
-    """Run ssd_bwd. Returns dict of gradients (None where the input is absent)."""
+    """Run ssd_bwd. Returns dict of gradients (None where the input is absent).
+    ``A`` is the decay input the forward took (A_cumsum with a cache)."""
     lib = C_.load()
     desc = _desc(cfg, x, B, dt, D, z, init, has_dfinal=dfinal is not None)
     dev = x.device
@@ -133,7 +147,7 @@ def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal
     g = {
         "x": torch.empty_like(x), "B": torch.empty_like(B), "C": torch.empty_like(C),
         "dt": torch.empty_like(dt) if dt is not None else None,
-        "A": (torch.empty_like(A) if cfg.a_mode in (C_.SSD_A_PER_HEAD, C_.SSD_A_PER_TOKEN) else None),
+        "A": _dA_out(cfg, x, A),
         "D": torch.empty_like(D) if D is not None else None,
         "z": torch.empty_like(z) if z is not None else None,
         "w": torch.empty_like(w) if (w is not None and z is not None) else None,
@@ -154,28 +168,31 @@ def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal
 
 
 class _SsdFunction(torch.autograd.Function):
-    """Autograd node over ssd_fwd / ssd_bwd (inputs already contiguous)."""
+    """Autograd node over ssd_fwd / ssd_bwd (inputs already contiguous). With ``acs`` (a cached
+    A_cumsum, cfg.a_mode CUMSUM) the kernels take the decay from it and ``A`` (per token) only
+    receives the gradient terms cfg.dA_skip leaves in."""
 
     @staticmethod
-    def forward(ctx, cfg, x, dt, A, B, C, D, z, w, init, cu):
+    def forward(ctx, cfg, x, dt, A, B, C, D, z, w, init, cu, acs=None):
         ctx.set_materialize_grads(False)
-        y, final, acs, saved = _forward(cfg, x, dt, A, B, C, D, z, w, init, cu)
+        a_arg = acs if cfg.a_mode == C_.SSD_A_CUMSUM else A
+        y, final, acs_out, saved = _forward(cfg, x, dt, a_arg, B, C, D, z, w, init, cu)
         ctx.cfg = cfg
         ctx.ws = saved
-        ctx.save_for_backward(x, dt, A, B, C, D, z, w, init, cu)
-        ctx.mark_non_differentiable(acs)
-        return y, final, acs
+        ctx.save_for_backward(x, dt, a_arg, B, C, D, z, w, init, cu)
+        ctx.mark_non_differentiable(acs_out)
+        return y, final, acs_out
 
     @staticmethod
     def backward(ctx, dy, dfinal, _dacs):
-        x, dt, A, B, C, D, z, w, init, cu = ctx.saved_tensors
+        x, dt, a_arg, B, C, D, z, w, init, cu = ctx.saved_tensors
         if dy is None and dfinal is None:
-            return (None,) * 11
-        g = _backward(ctx.cfg, ctx.ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal)
+            return (None,) * 12
+        g = _backward(ctx.cfg, ctx.ws, x, dt, a_arg, B, C, D, z, w, init, cu, dy, dfinal)
         ni = ctx.needs_input_grad
         pick = lambda k, i: g[k] if ni[i] else None  # noqa: E731
         return (None, pick("x", 1), pick("dt", 2), pick("A", 3), pick("B", 4), pick("C", 5),
-                pick("D", 6), pick("z", 7), pick("w", 8), pick("init", 9), None)
+                pick("D", 6), pick("z", 7), pick("w", 8), pick("init", 9), None, None)
 
 
 # --------------------------------------------------------------------------- #
@@ -245,11 +262,6 @@ class _LazyCache(dict):
         return dict.__getitem__(self, "A_cumsum")
 
 
-def _reference_cfg(x, chunk, a_mode, want_acs):
-    return _Cfg(chunk=chunk, a_mode=a_mode, nseq=x.shape[0], varlen=False,
-                state_code=_code(x.dtype, "x"), want_acs=want_acs, eps=0.0)
-
-
 def _check_reference_inputs(x, A, B, C, chunk_size):
     assert x.shape[1] % chunk_size == 0, (
         f"sequence length {x.shape[1]} not divisible by chunk_size {chunk_size}")
@@ -257,6 +269,47 @@ def _check_reference_inputs(x, A, B, C, chunk_size):
     if not (x.dtype == A.dtype == B.dtype == C.dtype):
         raise RuntimeError(f"fused_ssd_scan: x, A, B, C must share one dtype "
                            f"(got {x.dtype}, {A.dtype}, {B.dtype}, {C.dtype})")
+
+
+def _check_cached(name, t, shape, x):
+    """A cached tensor must be what a prior call on inputs of x's shape returned: the reference
+    combines it with this call's tensors in torch ops, which raise RuntimeError on a shape or
+    dtype mismatch (ssd_scan.py:364-408); the kernels read A_cumsum by that shape."""
+    if tuple(t.shape) != tuple(shape) or t.dtype != x.dtype:
+        raise RuntimeError(f"fused_ssd_scan: cached {name} has shape {tuple(t.shape)} and dtype {t.dtype}; "
+                           f"this call needs {tuple(shape)} and {x.dtype}")
+    _check_device(t)
+    if t.device != x.device:
+        raise RuntimeError(f"fused_ssd_scan: cached {name} is on {t.device}, the inputs on {x.device}")
+
+
+@dataclass(frozen=True)
+class _CachePlan:
+    cfg: _Cfg
+    acs: torch.Tensor | None   # the cached A_cumsum the kernels read, or None (cumsum of A)
+    A_used: bool               # A enters the computation (else its gradient is None, as in :533)
+
+
+def _cache_plan(x, A, chunk, has_L, has_dc, acs):
+    """Which decays come from a cache (ssd_scan.py:364-406): the intra-chunk L, the inter-chunk
+    decay_chunk, A_cumsum (state build, Y_off, and decay_chunk when not cached itself). A cached
+    tensor takes no gradient, so each one drops its terms from dA; A takes none at all when it feeds
+    nothing (L and A_cumsum both cached). The kernels compute every decay from A_cumsum (the cached
+    one, or the cumsum of A): a cached L or decay_chunk is taken to be the one a call on the same
+    decays returned, which is how the reference's caller builds its cache
+    (mamba_base_engine.py:170-181)."""
+    b, T, H = x.shape[:3]
+    nch = T // chunk
+    if acs is not None:
+        _check_cached("A_cumsum", acs, (b, H, nch, chunk), x)
+    skip = ((C_.SSD_DA_SKIP_INTRA if has_L else 0)
+            | (C_.SSD_DA_SKIP_CUMSUM | C_.SSD_DA_SKIP_CHUNK if acs is not None else 0)
+            | (C_.SSD_DA_SKIP_CHUNK if has_dc else 0))
+    a_mode = C_.SSD_A_CUMSUM if acs is not None else C_.SSD_A_PER_TOKEN
+    cfg = _Cfg(chunk=chunk, a_mode=a_mode, nseq=b, varlen=False, state_code=_code(x.dtype, "x"),
+               want_acs=acs is None, eps=0.0, dA_skip=skip)
+    return _CachePlan(cfg, None if acs is None else acs.detach().contiguous(),
+                      not (has_L and acs is not None))
 
 
 def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
@@ -268,41 +321,56 @@ def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
         B, C: (b, seqlen, n_heads, d_state), same dtype.
         chunk_size: seqlen must be divisible by this (AssertionError otherwise).
         initial_states: optional (b, 1, n_heads, d_head, d_state); zeros if None.
-        cache: optional dict from a prior call; its A_cumsum replaces A, and A
-            then receives no gradient (as in the reference).
+        cache: optional dict from a prior call with any of the keys L, decay_chunk,
+            A_cumsum (None values count as absent). Each cached decay replaces the one
+            computed from A and carries no gradient, as in the reference: with the whole
+            cache of a prior call (the β call of the Mamba-3 block), A gets no gradient.
 
     Returns:
         Y (b, seqlen, n_heads, d_head), final_state (b, n_heads, d_head, d_state),
-        cache {L, decay_chunk, A_cumsum}.
+        cache {L, decay_chunk, A_cumsum}; L and decay_chunk are computed on first access.
     """
     chunk = int(chunk_size)
     _check_reference_inputs(x, A, B, C, chunk)
     b, T, H, P = x.shape
     N = B.shape[-1]
     init = None if initial_states is None else initial_states.reshape(b, H, P, N).contiguous()
-    if cache is not None:
-        acs = cache.cumsum_tensor() if isinstance(cache, _LazyCache) else cache.get("A_cumsum")
-        if acs is None:
-            raise NotImplementedError("fused_ssd_scan: a cache without A_cumsum is not supported")
-        cfg = _reference_cfg(x, chunk, C_.SSD_A_CUMSUM, False)
-        Y, final, _ = _SsdFunction.apply(cfg, x.contiguous(), None, acs.detach().contiguous(), B.contiguous(),
-                                         C.contiguous(), None, None, None, init, None)
-        out = cache.copy() if isinstance(cache, _LazyCache) else {
-            "L": cache.get("L"), "decay_chunk": cache.get("decay_chunk"), "A_cumsum": acs}
-        return Y, final, out
-    cfg = _reference_cfg(x, chunk, C_.SSD_A_PER_TOKEN, True)
+    L_in = dc_in = acs_in = None
+    if isinstance(cache, _LazyCache):
+        # every key is present (L and decay_chunk lazily, from the same decays)
+        has_L = has_dc = True
+        acs_in = cache.cumsum_tensor()
+    elif cache is not None:
+        L_in, dc_in, acs_in = cache.get("L"), cache.get("decay_chunk"), cache.get("A_cumsum")
+        has_L, has_dc = L_in is not None, dc_in is not None
+        nch = T // chunk
+        if has_L:
+            _check_cached("L", L_in, (b, H, nch, chunk, chunk), x)
+        if has_dc:
+            _check_cached("decay_chunk", dc_in, (b, H, nch + 1, nch + 1), x)
+    else:
+        has_L = has_dc = False
+    plan = _cache_plan(x, A, chunk, has_L, has_dc, acs_in)
     a = A.contiguous()
-    Y, final, acs = _SsdFunction.apply(cfg, x.contiguous(), None, a, B.contiguous(), C.contiguous(), None, None,
-                                       None, init, None)
-    return Y, final, _LazyCache(a.detach(), acs, chunk)
+    Y, final, acs = _SsdFunction.apply(plan.cfg, x.contiguous(), None, a if plan.A_used else a.detach(),
+                                       B.contiguous(), C.contiguous(), None, None, None, init, None, plan.acs)
+    if isinstance(cache, _LazyCache):
+        return Y, final, cache.copy()
+    out = _LazyCache(a.detach(), acs if plan.acs is None else acs_in, chunk)
+    if L_in is not None:
+        dict.__setitem__(out, "L", L_in)
+    if dc_in is not None:
+        dict.__setitem__(out, "decay_chunk", dc_in)
+    return Y, final, out
 
 
 class FusedSSDScan(torch.autograd.Function):
     """The reference's autograd op with its exact 9-in / 5-out contract
-    (ssd_scan.py:427-533). L and decay_chunk are returned as tensors (the
-    cached ones when given). With A_cumsum supplied the decay comes from it
-    and dA is None; L / decay_chunk caches without A_cumsum are recomputed
-    from A (the kernels never read L)."""
+    (ssd_scan.py:427-533). Returns (Y, final_state, L, decay_chunk, A_cumsum): each
+    cached tensor as given, the others computed (L from A, decay_chunk from A_cumsum,
+    as the reference builds them). Backward returns the nine slots of :533; dA holds
+    the terms of the decays not taken from a cache, and is None when A feeds nothing
+    (L and A_cumsum both cached)."""
 
     @staticmethod
     def forward(ctx, x, A, B, C, chunk_size, initial_states, L_cache_in, decay_chunk_cache_in,
@@ -311,23 +379,26 @@ class FusedSSDScan(torch.autograd.Function):
         _check_reference_inputs(x, A, B, C, chunk)
         b, T, H, P = x.shape
         N = B.shape[-1]
+        nch = T // chunk
+        if L_cache_in is not None:
+            _check_cached("L", L_cache_in, (b, H, nch, chunk, chunk), x)
+        if decay_chunk_cache_in is not None:
+            _check_cached("decay_chunk", decay_chunk_cache_in, (b, H, nch + 1, nch + 1), x)
         init = None if initial_states is None else initial_states.reshape(b, H, P, N).contiguous()
         x, B, C = x.contiguous(), B.contiguous(), C.contiguous()
-        if A_cumsum_cache_in is not None:
-            cfg = _reference_cfg(x, chunk, C_.SSD_A_CUMSUM, False)
-            a_arg = A_cumsum_cache_in.detach().contiguous()
-        else:
-            cfg = _reference_cfg(x, chunk, C_.SSD_A_PER_TOKEN, True)
-            a_arg = A.detach().contiguous()
-        Y, final, acs, saved = _forward(cfg, x, None, a_arg, B, C, None, None, None, init, None)
+        plan = _cache_plan(x, A, chunk, L_cache_in is not None, decay_chunk_cache_in is not None,
+                           A_cumsum_cache_in)
+        a_tok = A.detach().contiguous()
+        a_arg = plan.acs if plan.acs is not None else a_tok
+        Y, final, acs, saved = _forward(plan.cfg, x, None, a_arg, B, C, None, None, None, init, None)
         if A_cumsum_cache_in is not None:
             acs = A_cumsum_cache_in
-        lazy = _LazyCache(A.detach().contiguous(), acs, chunk)
+        lazy = _LazyCache(a_tok, acs, chunk)
         L = L_cache_in if L_cache_in is not None else lazy["L"]
         dc = decay_chunk_cache_in if decay_chunk_cache_in is not None else lazy["decay_chunk"]
-        ctx.cfg = cfg
+        ctx.cfg = plan.cfg
+        ctx.A_used = plan.A_used
         ctx.ws = saved
-        ctx.has_init = initial_states is not None
         ctx.init_shape = None if initial_states is None else initial_states.shape
         ctx.save_for_backward(x, a_arg, B, C, init)
         ctx.set_materialize_grads(False)
@@ -340,8 +411,8 @@ class FusedSSDScan(torch.autograd.Function):
             return (None,) * 9
         g = _backward(ctx.cfg, ctx.ws, x, None, a_arg, B, C, None, None, None, init, None, dY, dfinal_state)
         ni = ctx.needs_input_grad
-        dA = g["A"] if (ni[1] and ctx.cfg.a_mode == C_.SSD_A_PER_TOKEN) else None
-        dinit = g["init"].reshape(ctx.init_shape) if (ctx.has_init and ni[5]) else None
+        dA = g["A"] if (ni[1] and ctx.A_used) else None
+        dinit = g["init"].reshape(ctx.init_shape) if (ctx.init_shape is not None and ni[5]) else None
         return (g["x"] if ni[0] else None, dA, g["B"] if ni[2] else None, g["C"] if ni[3] else None,
                 None, dinit, None, None, None)
 
@@ -377,5 +448,5 @@ def ssd_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, norm_weight=No
     init = f32(initial_states)
     out, final, _ = _SsdFunction.apply(cfg, x.contiguous(), f32(dt), f32(A), B.contiguous(), C.contiguous(),
                                        f32(D), None if z is None else z.contiguous(),
-                                       f32(norm_weight) if z is not None else None, init, cu)
+                                       f32(norm_weight) if z is not None else None, init, cu, None)
     return (out, final) if return_final_state else out

@@ -25,7 +25,8 @@
  *   dt, ddt                   (batch, seqlen, nheads)                 fp32
  *   A, dA  a_mode PER_HEAD    (nheads,)                               fp32
  *          a_mode PER_TOKEN   (batch, seqlen, nheads)                 dtype  (log-decay a = A, no dt)
- *          a_mode CUMSUM      (batch, nheads, nchunks, chunk)         dtype  (the reference's A_cumsum)
+ *          a_mode CUMSUM      (batch, nheads, nchunks, chunk)         dtype  (the reference's A_cumsum);
+ *                             dA is then (batch, seqlen, nheads) in dtype, see dA_skip
  *   D, dD                     (nheads,)                               fp32
  *   norm_weight, dnorm_weight (nheads*headdim,)                       fp32
  *   init, final, dinit, dfinal(nseq, nheads, headdim, dstate)         state_dtype
@@ -63,8 +64,22 @@ enum ssd_dtype { SSD_DTYPE_F32 = 0, SSD_DTYPE_BF16 = 1 };
 enum ssd_a_mode {
   SSD_A_PER_HEAD = 0,   /* a = dt * A[h]                        (extended API) */
   SSD_A_PER_TOKEN = 1,  /* a = A[b, t, h], dt absent            (reference API) */
-  SSD_A_CUMSUM = 2      /* a's in-chunk inclusive cumsum given; no dA computed
-                           (reference cache path, ssd_scan.py:364-366, :533)   */
+  SSD_A_CUMSUM = 2      /* a's in-chunk inclusive cumsum given (reference cache path,
+                           ssd_scan.py:364-366); dA needs dA_skip below          */
+};
+
+/* Terms of the log-decay gradient left out, one bit per place the reference
+ * op takes its decay from a cache instead of from A (ssd_scan.py:364-406; a
+ * cached tensor receives no gradient, :533):
+ *   INTRA   the intra-chunk decay L            (L cached,           :370-382)
+ *   CUMSUM  the state-build and output decays  (A_cumsum cached,    :364-368, :389-391, :414)
+ *   CHUNK   the inter-chunk decay_chunk        (decay_chunk or A_cumsum cached, :399-406)
+ * a_mode CUMSUM requires CUMSUM and CHUNK; its dA (per token) then holds the
+ * INTRA term when that bit is clear, and is not written when it is set. */
+enum ssd_dA_skip {
+  SSD_DA_SKIP_INTRA = 1,
+  SSD_DA_SKIP_CUMSUM = 2,
+  SSD_DA_SKIP_CHUNK = 4
 };
 
 /* Kernel limits: chunk <= 256, headdim <= 128, dstate <= 128. */
@@ -82,6 +97,7 @@ typedef struct ssd_desc {
   int32_t want_final;    /* ssd_fwd writes final_state                               */
   int32_t want_A_cumsum; /* ssd_fwd writes A_cumsum_out (needs varlen == 0)          */
   float norm_eps;        /* gated RMSNorm epsilon (has_z)                            */
+  int32_t dA_skip;       /* enum ssd_dA_skip bits; 0: the full gradient              */
 } ssd_desc_t;
 
 /* Kernel launches of ssd_fwd / ssd_bwd, in launch order. For profiling, a

@@ -87,6 +87,10 @@ def test_validation_accepts_benchmark_configs(capi):
     # reference API: per-token A, no dt, state in the input dtype
     assert _validate(capi, a_mode=capi.SSD_A_PER_TOKEN, has_dt=0, has_D=0, has_z=0, ngroups=64,
                      state_dtype=capi.SSD_DTYPE_BF16, want_A_cumsum=1) == capi.SSD_OK
+    # reference cache path: cached A_cumsum, with and without a cached L
+    for skip in (6, 7):
+        assert _validate(capi, a_mode=capi.SSD_A_CUMSUM, has_dt=0, has_D=0, has_z=0, ngroups=64,
+                         dA_skip=skip) == capi.SSD_OK
 
 
 @pytest.mark.parametrize("kw,status", [
@@ -98,6 +102,10 @@ def test_validation_accepts_benchmark_configs(capi):
     (dict(a_mode=2, has_dt=0, seqlen=8000), "SSD_ERR_INVALID"),  # cumsum path needs T % Q == 0
     (dict(want_A_cumsum=1, varlen=1, batch=1, nseq=2), "SSD_ERR_INVALID"),
     (dict(norm_eps=float("nan")), "SSD_ERR_INVALID"),
+    (dict(dA_skip=8), "SSD_ERR_INVALID"),                       # unknown dA_skip bit
+    # a cached A_cumsum (cumsum mode) carries no gradient: CUMSUM and CHUNK must be skipped
+    (dict(a_mode=2, has_dt=0, dA_skip=0), "SSD_ERR_INVALID"),
+    (dict(a_mode=2, has_dt=0, dA_skip=2), "SSD_ERR_INVALID"),
     (dict(chunk=512), "SSD_ERR_UNSUPPORTED"),
     (dict(headdim=256), "SSD_ERR_UNSUPPORTED"),
     (dict(dstate=160), "SSD_ERR_UNSUPPORTED"),
@@ -153,6 +161,41 @@ def test_product_path_refuses_cpu_tensors():
         kernels.fused_ssd_scan(x, A, B, B, 32)
     with pytest.raises(AssertionError):
         kernels.ssd_scan_combined(x, A.abs(), -torch.ones(2), B, B, 32)
+
+
+def test_cached_tensor_rejections():
+    """A cache from a call of another shape or dtype raises as the reference's torch ops would
+    (RuntimeError); a CPU tensor fails the device assertion. No GPU calls."""
+    import torch
+    from kernels import ssd_scan as ks
+    x = torch.zeros(2, 256, 4, 8)
+    good = (2, 4, 4, 64)
+    with pytest.raises(RuntimeError):
+        ks._check_cached("A_cumsum", torch.zeros(2, 4, 2, 128), good, x)       # other chunking
+    with pytest.raises(RuntimeError):
+        ks._check_cached("A_cumsum", torch.zeros(1, 4, 4, 64), good, x)        # other batch
+    with pytest.raises(RuntimeError):
+        ks._check_cached("A_cumsum", torch.zeros(good, dtype=torch.bfloat16), good, x)
+    with pytest.raises(AssertionError):
+        ks._check_cached("A_cumsum", torch.zeros(good), good, x)               # CPU tensor
+
+
+def test_cache_plan_gradient_terms(capi):
+    """Which dA terms each cache combination leaves out (ssd_scan.py:364-406, :533)."""
+    import torch
+    from kernels import ssd_scan as ks
+    x, A = torch.zeros(1, 128, 2, 8), torch.zeros(1, 128, 2)
+    I, S, K = capi.SSD_DA_SKIP_INTRA, capi.SSD_DA_SKIP_CUMSUM, capi.SSD_DA_SKIP_CHUNK
+    cases = {(False, False): (0, True), (True, False): (I, True), (False, True): (K, True),
+             (True, True): (I | K, True)}
+    for (has_L, has_dc), (skip, used) in cases.items():
+        p = ks._cache_plan(x, A, 64, has_L, has_dc, None)
+        assert p.cfg.dA_skip == skip and p.A_used == used and p.cfg.a_mode == capi.SSD_A_PER_TOKEN
+    # with a cached A_cumsum the device check comes last, so build the plan from its parts
+    for has_L in (False, True):
+        skip = (I if has_L else 0) | S | K
+        assert capi.load().ssd_validate(ctypes.byref(_desc(capi, a_mode=capi.SSD_A_CUMSUM, has_dt=0, has_D=0,
+                                                              has_z=0, ngroups=64, dA_skip=skip))) == capi.SSD_OK
 
 
 def test_product_path_never_imports_the_oracle():

@@ -1,0 +1,181 @@
+"""GPU parity of the exported autograd op and the chunk-size edge cases.
+
+* ``FusedSSDScan.apply`` with its exact 9-in / 5-out contract (r2/dhammic-ai/
+  src/kernels/ssd_scan.py:427-533), for every combination of cached L,
+  decay_chunk and A_cumsum, with initial_states and a final-state gradient:
+  all 5 outputs and all 9 backward slots against the oracle's restatement of
+  ``_ssd_forward_impl`` (:330-421) differentiated by autograd.
+* chunk = 192: three positions per lane in the per-(chunk, head) kernels, so
+  a lane's positions straddle two 64-token blocks; ddt / dA checked per head.
+* a single steep decay at token 96 of a chunk (inside the middle 64-token
+  block of a 192-token chunk), which must send that (chunk, head) to the
+  exact path.
+Tolerances (normwise max|d| / max|ref|): 1e-4 fp32, 1e-2 bf16.
+"""
+from __future__ import annotations
+
+import itertools
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from oracle import ssd_chunked as oc
+from oracle.inputs import SsdShape, make_inputs, make_reference_test_inputs
+from ssd_testlib import TOL, assert_close, oracle_extended
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs an MI355X (HIP device)")]
+
+DEV = "cuda"
+COMBOS = [c for r in range(4) for c in itertools.combinations(("L", "decay_chunk", "A_cumsum"), r)]
+
+
+def _k():
+    import kernels
+    return kernels
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("cached", COMBOS, ids=lambda c: "+".join(c) or "none")
+def test_fused_ssd_scan_apply_contract(dtype, cached):
+    b, T, h, p, n, chunk = 2, 256, 4, 16, 8, 64
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=21)
+    x2, _, B2, C2 = make_reference_test_inputs(b, T, h, p, n, seed=22)
+    gen = torch.Generator().manual_seed(23)
+    init = torch.randn(b, 1, h, p, n, generator=gen) * 0.1
+    dY = torch.randn(b, T, h, p, generator=gen)
+    dF = torch.randn(b, h, p, n, generator=gen)
+    x, A, B, C, x2, B2, C2, init, dY, dF = [t.to(dtype).float() for t in (x, A, B, C, x2, B2, C2, init, dY, dF)]
+    k = _k()
+    # the cache of a prior call on the same decays (the Mamba-3 block's beta call)
+    _, _, c0 = k.fused_ssd_scan(*[t.to(DEV, dtype) for t in (x, A, B, C)], chunk)
+    cache = {key: c0[key].detach().clone() for key in cached}
+    # native: every input a leaf, the cached tensors too (they must get no gradient)
+    leaves = [t.to(DEV, dtype).requires_grad_(True) for t in (x2, A, B2, C2, init)]
+    cin = {key: v.requires_grad_(True) for key, v in cache.items()}
+    out = k.FusedSSDScan.apply(*leaves[:4], chunk, leaves[4], cin.get("L"), cin.get("decay_chunk"),
+                               cin.get("A_cumsum"))
+    assert len(out) == 5
+    torch.autograd.backward([out[0], out[1]], [dY.to(DEV, dtype), dF.to(DEV, dtype)])
+    # oracle in fp64 on the same (rounded) values
+    ol = [t.double().requires_grad_(True) for t in (x2, A, B2, C2, init)]
+    oc_in = {key: v.detach().cpu().double() for key, v in cache.items()}
+    Yo, fo, co = oc.ssd_forward_impl(*ol[:4], chunk, ol[4], oc_in.get("L"), oc_in.get("decay_chunk"),
+                                     oc_in.get("A_cumsum"))
+    torch.autograd.backward([Yo, fo], [dY.double(), dF.double()])
+    tol = TOL[dtype]
+    assert out[0].dtype == dtype and out[0].shape == (b, T, h, p)
+    assert out[1].shape == (b, h, p, n)
+    assert out[2].shape == (b, h, T // chunk, chunk, chunk)
+    assert out[3].shape == (b, h, T // chunk + 1, T // chunk + 1)
+    assert out[4].shape == (b, h, T // chunk, chunk)
+    assert_close("Y", out[0], Yo, tol)
+    assert_close("final_state", out[1], fo, tol)
+    assert_close("L", out[2], co["L"], tol)
+    assert_close("decay_chunk", out[3], co["decay_chunk"], tol)
+    assert_close("A_cumsum", out[4], co["A_cumsum"], tol)
+    for key in cached:  # a cached tensor comes back as given
+        assert out[("L", "decay_chunk", "A_cumsum").index(key) + 2].data_ptr() == cin[key].data_ptr()
+    for name, lv, ov in zip(("dx", "dA", "dB", "dC", "dinit"), leaves, ol):
+        if ov.grad is None:
+            assert lv.grad is None, f"{name}: the reference gives no gradient here"
+        else:
+            assert lv.grad is not None and lv.grad.shape == lv.shape, name
+            assert_close(name, lv.grad, ov.grad, tol)
+    for key, v in cin.items():
+        assert v.grad is None, key
+
+
+@pytest.mark.parametrize("cached", [("A_cumsum",), ("L", "decay_chunk")], ids=["acs", "L+dc"])
+def test_fused_ssd_scan_partial_cache_dict(cached):
+    """fused_ssd_scan with a cache dict holding only some keys (the reference reads each with
+    cache.get, ssd_scan.py:565-568): values and gradients against the oracle."""
+    b, T, h, p, n, chunk = 2, 256, 4, 16, 8, 64
+    x, A, B, C = make_reference_test_inputs(b, T, h, p, n, seed=31)
+    dY = torch.randn(b, T, h, p, generator=torch.Generator().manual_seed(32))
+    k = _k()
+    _, _, c0 = k.fused_ssd_scan(*[t.to(DEV) for t in (x, A, B, C)], chunk)
+    cache = {key: c0[key] for key in cached}
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x, A, B, C)]
+    Y, fin, cout = k.fused_ssd_scan(*leaves, chunk, cache=cache)
+    Y.backward(dY.to(DEV))
+    ol = [t.double().requires_grad_(True) for t in (x, A, B, C)]
+    Yo, fo, co = oc.fused_ssd_scan(*ol, chunk, cache={kk: v.cpu().double() for kk, v in cache.items()})
+    Yo.backward(dY.double())
+    tol = TOL[torch.float32]
+    assert_close("Y", Y, Yo, tol)
+    assert_close("final_state", fin, fo, tol)
+    for key in ("L", "decay_chunk", "A_cumsum"):
+        assert_close(key, cout[key], co[key], tol)
+    for name, lv, ov in zip(("dx", "dA", "dB", "dC"), leaves, ol):
+        assert (lv.grad is None) == (ov.grad is None), name
+        if ov.grad is not None:
+            assert_close(name, lv.grad, ov.grad, tol)
+
+
+def test_fused_ssd_scan_rejects_a_foreign_cache():
+    """A cache from a call with another chunking or dtype raises RuntimeError, as the
+    reference's torch ops on mismatched shapes do; nothing is launched."""
+    k = _k()
+    x, A, B, C = [t.to(DEV) for t in make_reference_test_inputs(1, 256, 2, 8, 4, seed=3)]
+    _, _, c128 = k.fused_ssd_scan(x, A, B, C, 128)
+    with pytest.raises(RuntimeError):
+        k.fused_ssd_scan(x, A, B, C, 64, cache={"A_cumsum": c128["A_cumsum"]})
+    with pytest.raises(RuntimeError):
+        k.fused_ssd_scan(x, A, B, C, 128, cache={"A_cumsum": c128["A_cumsum"].bfloat16()})
+    with pytest.raises(RuntimeError):
+        k.FusedSSDScan.apply(x, A, B, C, 64, None, c128["L"], None, None)
+
+
+def _run_ext(inp, chunk, dtype):
+    dev = {kk: v.to(DEV) for kk, v in inp.items()}
+    leaves = {kk: dev[kk].to(dtype).requires_grad_(True) for kk in ("x", "B", "C")}
+    for kk in ("dt", "A", "D", "init"):
+        leaves[kk] = dev[kk].requires_grad_(True)
+    out, fin = _k().ssd_scan_combined(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], chunk,
+                                      D=leaves["D"], initial_states=leaves["init"], return_final_state=True)
+    torch.autograd.backward([out, fin], [dev["dy"].to(dtype), dev["dfinal"]])
+    return out, fin, {kk: v.grad for kk, v in leaves.items()}
+
+
+def _per_head_check(shape, inp, dtype):
+    out, fin, g = _run_ext(inp, shape.chunk, dtype)
+    oo, fo, go = oracle_extended(inp, shape.chunk, init=inp["init"], dfinal=inp["dfinal"])
+    tol = TOL[dtype]
+    for hh in range(shape.nheads):
+        assert_close(f"out[h={hh}]", out[:, :, hh], oo[:, :, hh], tol)
+        assert_close(f"dx[h={hh}]", g["x"][:, :, hh], go["x"][:, :, hh], tol)
+        assert_close(f"ddt[h={hh}]", g["dt"][:, :, hh], go["dt"][:, :, hh], tol)
+        assert_close(f"final[h={hh}]", fin[:, hh], fo[:, hh], tol)
+        assert_close(f"dinit[h={hh}]", g["init"][:, hh], go["init"][:, hh], tol)
+        assert_close(f"dA[h={hh}]", g["A"][hh:hh + 1], go["A"][hh:hh + 1], tol)
+    for kk in ("D", "B", "C"):
+        assert_close("d" + kk, g[kk], go[kk], tol)
+
+
+def _ext_inputs(shape, seed, dtype):
+    inp = make_inputs(shape, seed=seed, with_init=True, with_dfinal=True)
+    for kk in ("x", "B", "C", "dy"):
+        inp[kk] = inp[kk].to(dtype).float()
+    return inp
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_chunk192_three_positions_per_lane(dtype):
+    """Qpad = 192: each lane of the finish kernel owns three positions, lane 21 holds 63..65 and
+    lane 42 holds 126..128, across the rowG partials of two column blocks."""
+    shape = SsdShape(2, 768, 4, 64, 1, 64, 192)
+    _per_head_check(shape, _ext_inputs(shape, 41, dtype), dtype)
+
+
+def test_chunk192_steep_decay_inside_a_block():
+    """One token with dt*|A| = 100 nats at position 96 of a 192-token chunk: block 1 (positions
+    64..127) drops by more than the factorisation range, so that (chunk, head) must take the exact
+    kernels; a per-lane window guard that misses the 95 -> 96 step would overflow exp()."""
+    shape = SsdShape(2, 768, 4, 64, 1, 64, 192)
+    inp = _ext_inputs(shape, 42, torch.bfloat16)
+    inp["A"][2] = -1.0
+    inp["dt"][0, 192 + 96, 2] = 100.0
+    inp["dt"][1, 96, 2] = 100.0
+    _per_head_check(shape, inp, torch.bfloat16)
