@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 
 #include "ssd_mi355x.h"
 #include "ssd_launch.h"
@@ -217,28 +218,8 @@ struct PhaseTimer {
     SSD_TRY((tm).end(ph));        \
   } while (0)
 
-}  // namespace
-
-extern "C" {
-
-int ssd_validate(const ssd_desc_t* desc) {
-  Plan p;
-  return plan(desc, &p);
-}
-
-size_t ssd_workspace_bytes(const ssd_desc_t* desc, int kind) {
-  Plan p;
-  if (plan(desc, &p) != SSD_OK) return 0;
-  switch (kind) {
-    case SSD_WS_SAVED: return p.saved_bytes;
-    case SSD_WS_FWD_SCRATCH: return p.fwd_bytes;
-    case SSD_WS_BWD_SCRATCH: return p.bwd_bytes;
-    default: return 0;
-  }
-}
-
-int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t saved_bytes, void* scratch,
-            size_t scratch_bytes, void* stream) {
+int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t saved_bytes, void* scratch,
+             size_t scratch_bytes, void* stream) {
   Plan p;
   int st = plan(desc, &p);
   if (st != SSD_OK) return st;
@@ -281,6 +262,69 @@ int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t
     SSD_PHASE(tm, SSD_PH_FWD_SCAN, launch_chunk_scan_fwd(p.dtype, d, b, in, yout, s));
   if (d.has_z) SSD_PHASE(tm, SSD_PH_NORM_FWD, launch_gated_norm_fwd(p.dtype, d, b, in, a->y, s));
   return SSD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Workspace of ssd_fwd_noalloc: one file-scope device array per GPU, allocated
+// with the code object when the library is first used on that GPU and held
+// until the process ends. Host code never passes the array's name to a kernel
+// (on the host it is a stand-in, not a device address): each device's address
+// comes from hipGetSymbolAddress, taken once with that device current.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[SSD_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (nullptr on a HIP error).
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssd_validate(const ssd_desc_t* desc) {
+  Plan p;
+  return plan(desc, &p);
+}
+
+size_t ssd_workspace_bytes(const ssd_desc_t* desc, int kind) {
+  Plan p;
+  if (plan(desc, &p) != SSD_OK) return 0;
+  switch (kind) {
+    case SSD_WS_SAVED: return p.saved_bytes;
+    case SSD_WS_FWD_SCRATCH: return p.fwd_bytes;
+    case SSD_WS_BWD_SCRATCH: return p.bwd_bytes;
+    default: return 0;
+  }
+}
+
+int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_t saved_bytes, void* scratch,
+            size_t scratch_bytes, void* stream) {
+  return fwd_impl(desc, a, saved, saved_bytes, scratch, scratch_bytes, stream);
+}
+
+int ssd_fwd_noalloc(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* stream) {
+  Plan p;
+  const int st = plan(desc, &p);
+  if (st != SSD_OK) return st;
+  // both forward workspaces, one after the other (the saved part is not kept for a backward)
+  const size_t off = align_up(p.saved_bytes);
+  if (off + p.fwd_bytes > (size_t)SSD_NOALLOC_SCRATCH_BYTES) return SSD_ERR_TOO_LARGE;
+  unsigned char* base = static_cast<unsigned char*>(scratch_on_current_device());
+  if (!base) return SSD_ERR_HIP;
+  return fwd_impl(desc, a, base, p.saved_bytes, base + off, p.fwd_bytes, stream);
 }
 
 int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, size_t saved_bytes, void* scratch,
@@ -389,10 +433,11 @@ const char* ssd_status_string(int status) {
     case SSD_ERR_UNSUPPORTED: return "unsupported shape or option";
     case SSD_ERR_WORKSPACE: return "workspace missing or too small";
     case SSD_ERR_HIP: return "HIP launch error";
+    case SSD_ERR_TOO_LARGE: return "input exceeds the no-allocation scratch (SSD_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
 
-int ssd_abi_version(void) { return 2; }
+int ssd_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -19,6 +19,10 @@ SSD_ERR_INVALID = -1
 SSD_ERR_UNSUPPORTED = -2
 SSD_ERR_WORKSPACE = -3
 SSD_ERR_HIP = -4
+SSD_ERR_TOO_LARGE = -5
+
+# ssd_fwd_noalloc's per-GPU scratch
+SSD_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 SSD_DTYPE_F32 = 0
 SSD_DTYPE_BF16 = 1
@@ -41,7 +45,7 @@ SSD_WS_SAVED = 0
 SSD_WS_FWD_SCRATCH = 1
 SSD_WS_BWD_SCRATCH = 2
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -76,7 +80,7 @@ class SsdBwdArgs(ctypes.Structure):
 
 
 # Every symbol include/ssd_mi355x.h declares.
-EXPORTS = ("ssd_validate", "ssd_workspace_bytes", "ssd_fwd", "ssd_bwd", "ssd_materialize_L",
+EXPORTS = ("ssd_validate", "ssd_workspace_bytes", "ssd_fwd", "ssd_fwd_noalloc", "ssd_bwd", "ssd_materialize_L",
            "ssd_decay_chunk", "ssd_status_string", "ssd_abi_version")
 
 _lib = None
@@ -98,6 +102,8 @@ def load():
     lib.ssd_workspace_bytes.restype = ctypes.c_size_t
     lib.ssd_fwd.argtypes = [P(SsdDesc), P(SsdFwdArgs), _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]
     lib.ssd_fwd.restype = ctypes.c_int
+    lib.ssd_fwd_noalloc.argtypes = [P(SsdDesc), P(SsdFwdArgs), _vp]
+    lib.ssd_fwd_noalloc.restype = ctypes.c_int
     lib.ssd_bwd.argtypes = [P(SsdDesc), P(SsdBwdArgs), _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]
     lib.ssd_bwd.restype = ctypes.c_int
     lib.ssd_materialize_L.argtypes = [P(SsdDesc), _vp, _vp, _vp]

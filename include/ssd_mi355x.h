@@ -56,7 +56,8 @@ enum ssd_status {
   SSD_ERR_INVALID = -1,      /* bad shape, pointer or flag combination        */
   SSD_ERR_UNSUPPORTED = -2,  /* valid for the reference, outside kernel limits */
   SSD_ERR_WORKSPACE = -3,    /* workspace pointer missing or too small        */
-  SSD_ERR_HIP = -4           /* a HIP launch reported an error                */
+  SSD_ERR_HIP = -4,          /* a HIP launch reported an error                */
+  SSD_ERR_TOO_LARGE = -5     /* ssd_fwd_noalloc: workspace beyond its scratch */
 };
 
 enum ssd_dtype { SSD_DTYPE_F32 = 0, SSD_DTYPE_BF16 = 1 };
@@ -148,6 +149,19 @@ size_t ssd_workspace_bytes(const ssd_desc_t* desc, int kind);
 int ssd_fwd(const ssd_desc_t* desc, const ssd_fwd_args_t* args,
             void* saved, size_t saved_bytes, void* scratch, size_t scratch_bytes,
             void* stream);
+
+/* Forward without any allocation: as ssd_fwd, with both forward workspaces in a
+ * file-scope device array of SSD_NOALLOC_SCRATCH_BYTES per GPU (allocated with
+ * the library's code object and held until the process ends). No counterpart in
+ * the reference: it is for callers that cannot allocate (HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). Forward only (nothing is kept
+ * for ssd_bwd). Returns SSD_ERR_TOO_LARGE when ssd_workspace_bytes(SAVED),
+ * rounded up to 256 bytes, plus ssd_workspace_bytes(FWD_SCRATCH) exceeds the
+ * scratch. Every call on one GPU shares that GPU's array: calls that overlap on
+ * one GPU (other streams, other threads) race; the forward writes every part of
+ * the array it reads, so nothing is cleared between calls. */
+#define SSD_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ssd_fwd_noalloc(const ssd_desc_t* desc, const ssd_fwd_args_t* args, void* stream);
 
 /* Backward: all requested gradients (a NULL output pointer skips that output,
  * except dx, dB, dC which are required). `saved` must be the buffer the

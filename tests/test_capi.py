@@ -49,12 +49,14 @@ def test_ctypes_layout_matches_header(tmp_path, capi):
         lines.append(f'printf("{st} %zu\\n", sizeof({st}));')
         for f in fs:
             lines.append(f'printf("{st}.{f} %zu\\n", offsetof({st}, {f}));')
+    lines.append('printf("SSD_NOALLOC_SCRATCH_BYTES %zu\\n", (size_t)SSD_NOALLOC_SCRATCH_BYTES);')
     lines.append("return 0;}")
     src.write_text("\n".join(lines))
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
     out = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
                                                           check=True).stdout.splitlines())
+    assert int(out["SSD_NOALLOC_SCRATCH_BYTES"]) == capi.SSD_NOALLOC_SCRATCH_BYTES
     for st, cls in (("ssd_desc_t", capi.SsdDesc), ("ssd_fwd_args_t", capi.SsdFwdArgs),
                     ("ssd_bwd_args_t", capi.SsdBwdArgs)):
         assert int(out[st]) == ctypes.sizeof(cls), st
@@ -140,6 +142,21 @@ def test_entry_points_reject_null_pointers_without_touching_the_gpu(capi):
     args = capi.SsdFwdArgs(fake, fake, fake, fake, fake, fake, fake, fake, None, None, fake, fake, None)
     assert lib.ssd_fwd(ctypes.byref(d), ctypes.byref(args), None, 0, None, 0, None) == capi.SSD_ERR_WORKSPACE
     assert lib.ssd_status_string(capi.SSD_ERR_WORKSPACE) == b"workspace missing or too small"
+
+
+def test_noalloc_rejects_inputs_beyond_its_scratch_without_touching_the_gpu(capi):
+    """ssd_fwd_noalloc checks the workspace against its fixed scratch before any device call."""
+    lib = capi.load()
+    d = _desc(capi)                                   # config 2: far more than the scratch
+    fake = ctypes.c_void_p(16)
+    args = capi.SsdFwdArgs(fake, fake, fake, fake, fake, fake, fake, fake, None, None, fake, fake, None)
+    need = (lib.ssd_workspace_bytes(ctypes.byref(d), capi.SSD_WS_SAVED) + 255) // 256 * 256 + \
+        lib.ssd_workspace_bytes(ctypes.byref(d), capi.SSD_WS_FWD_SCRATCH)
+    assert need > capi.SSD_NOALLOC_SCRATCH_BYTES
+    assert lib.ssd_fwd_noalloc(ctypes.byref(d), ctypes.byref(args), None) == capi.SSD_ERR_TOO_LARGE
+    assert b"no-allocation scratch" in lib.ssd_status_string(capi.SSD_ERR_TOO_LARGE)
+    assert lib.ssd_fwd_noalloc(ctypes.byref(_desc(capi, batch=0)), ctypes.byref(args), None) == \
+        capi.SSD_ERR_INVALID
 
 
 def test_python_layer_maps_status_to_exceptions(capi):
