@@ -139,14 +139,29 @@ COPY_PROBE_BYTES = 1 << 30
 
 
 def copy_probe(dev):
-    """One plain device copy of COPY_PROBE_BYTES (read once, written once):
-    the calibration dispatch for the FETCH_SIZE / WRITE_SIZE counter runs."""
+    """Plain device copies of COPY_PROBE_BYTES each (read once, written once): the
+    calibration dispatches for the FETCH_SIZE / WRITE_SIZE counter runs. torch's
+    copy kernel, then the probe library's copy through buffer_load ... lds (the read
+    path of the DMA-ring kernels) and its 16-byte vector-load copy."""
+    import ctypes
     import torch
     src = torch.ones(COPY_PROBE_BYTES // 4, device=dev, dtype=torch.float32)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
+    lib = ctypes.CDLL(str(ROOT / "dhammic-ai_amd" / "kernels" / "libssd_probe.so"))
+    lib.ssd_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    lib.ssd_probe_copy.restype = ctypes.c_int
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    for mode in (0, 1):
+        dst.zero_()
+        torch.cuda.synchronize()
+        rc = lib.ssd_probe_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), COPY_PROBE_BYTES,
+                                mode, stream)
+        torch.cuda.synchronize()
+        if rc != 0 or not torch.equal(dst, src):
+            raise RuntimeError(f"copy probe mode {mode} failed (rc {rc})")
     del src, dst
 
 

@@ -19,6 +19,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "kernels" / "libssd_mi355x.so"
+# traffic-counter calibration copies for bench.py --copy-probe (not part of the SSD library)
+PROBE_SRC = PKG / "probe" / "ssd_probe.hip"
+PROBE_LIB = PKG / "kernels" / "libssd_probe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -63,6 +66,9 @@ def build(jobs: int = 8, verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
+    ptmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *CFLAGS, "-shared", "-o", str(ptmp), str(PROBE_SRC)], verbose)
+    os.replace(ptmp, PROBE_LIB)
     return LIB
 
 

@@ -1,0 +1,65 @@
+// Calibration copies for the HBM traffic counters (FETCH_SIZE / WRITE_SIZE):
+// a device copy whose reads go through buffer_load ... lds (the path of the
+// DMA-ring kernels) and one with plain 16-byte vector loads. Each reads and
+// writes `bytes` once. Not part of the SSD library's ABI: bench.py loads this
+// library only for --copy-probe.
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kStep = 4096;  // bytes per wave and iteration: four 1 KB DMA instructions
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0, 0x00020000);
+}
+
+// Wave w of the grid copies bytes [w * kStep, w * kStep + kStep), then strides by the grid's waves.
+// Each wave owns its 4 KB of LDS; the DMA is retired with vmcnt(0) before the wave reads it.
+__global__ void __launch_bounds__(kThreads) k_dma_copy(const unsigned char* __restrict__ src,
+                                                       unsigned char* __restrict__ dst, int64_t nsteps) {
+  __shared__ __align__(16) unsigned char buf[kThreads / 64][kStep];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t nw = (int64_t)gridDim.x * (kThreads / 64);
+  for (int64_t s = (int64_t)blockIdx.x * (kThreads / 64) + w; s < nsteps; s += nw) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(src + s * kStep);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(buf[w] + q * 1024), 16,
+                                               q * 1024 + lane * 16, 0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's DMA has landed in LDS
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = *reinterpret_cast<const uint4*>(buf[w] + q * 1024 + lane * 16);
+      *reinterpret_cast<uint4*>(dst + s * kStep + q * 1024 + lane * 16) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS reads done before the next DMA overwrites them
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) k_vec_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                       int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    dst[i] = src[i];
+}
+
+}  // namespace
+
+// mode 0: buffer_load ... lds copy, mode 1: 16-byte vector copy. bytes must be a multiple of 4096,
+// both pointers 16-byte aligned. Returns 0 on success, -1 on bad arguments, -4 on a launch error.
+extern "C" int ssd_probe_copy(const void* src, void* dst, size_t bytes, int mode, void* stream) {
+  if (!src || !dst || bytes == 0 || bytes % kStep || ((uintptr_t)src | (uintptr_t)dst) & 15) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid = 4096;
+  if (mode == 0)
+    hipLaunchKernelGGL(k_dma_copy, dim3(grid), dim3(kThreads), 0, s, static_cast<const unsigned char*>(src),
+                       static_cast<unsigned char*>(dst), (int64_t)(bytes / kStep));
+  else if (mode == 1)
+    hipLaunchKernelGGL(k_vec_copy, dim3(grid), dim3(kThreads), 0, s, static_cast<const uint4*>(src),
+                       static_cast<uint4*>(dst), (int64_t)(bytes / 16));
+  else
+    return -1;
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
