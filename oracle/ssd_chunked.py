@@ -90,12 +90,21 @@ def exp_clamp(x):
 
 
 def ssd_forward_impl(x, A, B, C, chunk_size, initial_states=None,
-                     L_cache=None, decay_chunk_cache=None, A_cumsum_cache=None):
+                     L_cache=None, decay_chunk_cache=None, A_cumsum_cache=None, storage=None):
     """Chunked SSD forward, ssd_scan.py:330-421.
 
     x (b,T,h,p), A (b,T,h), B/C (b,T,h,n); T % chunk_size == 0 (asserted, :348).
     Returns (Y (b,T,h,p), final_state (b,h,p,n), {L, decay_chunk, A_cumsum}).
+
+    ``storage`` (e.g. torch.bfloat16) emulates the reference run on inputs of that
+    dtype while computing in the inputs' (wider) dtype: every intermediate the
+    reference keeps as a tensor of the input dtype (A_cumsum, L, decay_states,
+    states, decay_chunk, new_states, state_decay_out, Y_diag, Y_off, Y) is rounded
+    to ``storage``, and so is its gradient (autograd through the two casts), while
+    each contraction accumulates in the wide dtype as the reference's bmm does.
     """
+    def st(t):
+        return t if storage is None else t.to(storage).to(t.dtype)
     assert x.shape[1] % chunk_size == 0, (
         f"sequence length {x.shape[1]} not divisible by chunk_size {chunk_size}")
     b, T = x.shape[0], x.shape[1]
@@ -106,15 +115,15 @@ def ssd_forward_impl(x, A, B, C, chunk_size, initial_states=None,
 
     x_c, A_c, B_c, C_c = chunk(x), chunk(A), chunk(B), chunk(C)
     A_perm = A_c.permute(0, 3, 1, 2)                              # (b,h,c,l)
-    A_cumsum = A_cumsum_cache if A_cumsum_cache is not None else torch.cumsum(A_perm, dim=-1)
+    A_cumsum = A_cumsum_cache if A_cumsum_cache is not None else st(torch.cumsum(A_perm, dim=-1))
 
     # step 1: intra-chunk diagonal blocks, L = exp(clamp(segsum(A))) (:370-385)
-    L = L_cache if L_cache is not None else exp_clamp(segsum(A_perm))
-    Y_diag = torch.einsum("bclhn,bcshn,bhcls,bcshp->bclhp", C_c, B_c, L, x_c)
+    L = L_cache if L_cache is not None else st(exp_clamp(st(segsum(A_perm))))
+    Y_diag = st(torch.einsum("bclhn,bcshn,bhcls,bcshp->bclhp", C_c, B_c, L, x_c))
 
     # step 2: per-chunk states (:387-392)
-    decay_states = exp_clamp(A_cumsum[..., -1:] - A_cumsum)
-    states = torch.einsum("bclhn,bhcl,bclhp->bchpn", B_c, decay_states, x_c)
+    decay_states = st(exp_clamp(st(A_cumsum[..., -1:] - A_cumsum)))
+    states = st(torch.einsum("bclhn,bhcl,bclhp->bchpn", B_c, decay_states, x_c))
 
     # step 3: inter-chunk recurrence in matrix form (:394-410)
     if initial_states is None:
@@ -123,18 +132,19 @@ def ssd_forward_impl(x, A, B, C, chunk_size, initial_states=None,
     if decay_chunk_cache is not None:
         decay_chunk = decay_chunk_cache
     else:
-        decay_chunk = exp_clamp(segsum(F.pad(A_cumsum[..., -1], (1, 0))))
-    new_states = torch.einsum("bhzc,bchpn->bzhpn", decay_chunk, states_full)
+        decay_chunk = st(exp_clamp(st(segsum(F.pad(A_cumsum[..., -1], (1, 0))))))
+    new_states = st(torch.einsum("bhzc,bchpn->bzhpn", decay_chunk, states_full))
     states_in, final_state = new_states[:, :-1], new_states[:, -1]
 
     # step 4: state -> output (:412-418)
-    Y_off = torch.einsum("bclhn,bchpn,bhcl->bclhp", C_c, states_in, exp_clamp(A_cumsum))
-    Y = (Y_diag + Y_off).reshape(b, T, *Y_diag.shape[3:])
+    Y_off = st(torch.einsum("bclhn,bchpn,bhcl->bclhp", C_c, states_in, st(exp_clamp(A_cumsum))))
+    Y = st(Y_diag + Y_off).reshape(b, T, *Y_diag.shape[3:])
     return Y, final_state, {"L": L, "decay_chunk": decay_chunk, "A_cumsum": A_cumsum}
 
 
-def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
-    """Reference public API (ssd_scan.py:539-583), plain autograd.
+def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None, storage=None):
+    """Reference public API (ssd_scan.py:539-583), plain autograd (``storage``: see
+    ssd_forward_impl).
 
     Gradients equal the reference's checkpointed backward (:467-533): with a
     cache, A is never read, so it receives no gradient; cache tensors never
@@ -149,7 +159,7 @@ def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
         ac_in = None if ac_in is None else ac_in.detach()
     else:
         L_in = dc_in = ac_in = None
-    return ssd_forward_impl(x, A, B, C, int(chunk_size), initial_states, L_in, dc_in, ac_in)
+    return ssd_forward_impl(x, A, B, C, int(chunk_size), initial_states, L_in, dc_in, ac_in, storage)
 
 
 def fused_ssd_scan_fwd_bwd_baseline(x, A, B, C, chunk_size, dY, initial_states=None):

@@ -1,18 +1,24 @@
-"""A small Mamba-3-style language model for the model-level parity test (test scaffolding only).
+"""A Mamba-3-style language model for the model-level parity tests (test scaffolding only).
 
-BASELINE config 4 is a full random-init training step of a 24-layer Mamba-3-style LM with the native SSD
-kernel swapped in, loss and per-layer gradients compared with the reference. This file restates, in plain
-PyTorch, the caller of the SSD in that model so the comparison can run at a reduced size:
+BASELINE config 4 is a full random-init training step of a 24-layer Mamba-3-style LM (d_model 1024, expand 2,
+H = 32, P = 64, N = 128, vocab 50 304, B = 4, L = 4096) with the native SSD kernel swapped in, loss and
+per-layer gradients compared with the reference. This file restates, in plain PyTorch, the model around the
+SSD so that the comparison runs the reference's own composition:
 
 * ``Mamba3Block`` follows ``r2/dhammic-ai/src/mamba_base_engine.py:34-192``: one in-projection split into
-  (z, x, B, C, dt_raw, lam_raw, theta) (:62-79), the trapezoidal coefficients (:143-145), RMSNorm on B and C
-  (:148-149), per-head data-dependent RoPE of B/C with learnable per-head biases (:152-167), padding to the
-  chunk (:172-182), the two SSD calls of the trapezoidal rule sharing the first call's cache (:186-197),
-  ``+ D x`` (:199-203) and the gated output norm and projection (:206-208).
-* ``trapezoidal`` follows ``src/kernels/trapezoidal.py:6-12``; ``rope`` follows ``src/kernels/rope.py:4-10``;
-  ``rmsnorm`` follows ``src/kernels/rmsnorm.py:222-229`` (fp32 statistics, output in the input dtype).
-* The model around the blocks (pre-norm residual layers with a SwiGLU MLP, a final RMSNorm, an untied LM head
-  and token cross-entropy) is config 4's description.
+  (z, x, B, C, dt_raw, lam_raw, theta) (:63-71, :124), the trapezoidal coefficients (:128-130), RMSNorm on B and
+  C (:133-134, eps 1e-6), per-head data-dependent RoPE of B/C with learnable per-head biases (:136-149),
+  padding to the chunk (:154-165), the two SSD calls of the trapezoidal rule, the second reusing the first
+  call's cache (:170-181), their sum (:183), ``+ D x`` (:187) and the gated output norm (eps 1e-6) and
+  projection (:190-192).
+* ``Layer`` follows ``MambaBlock`` (``src/citta_vithi_pipeline.py:159-190``): pre-norm residual layers with
+  RMSNorm eps 1e-5 (:168-169) and a SwiGLU MLP of width int(2.5 d) (:175); the model ends in a final RMSNorm,
+  eps 1e-5 (:290).
+* The loss is the tied LM head and token cross-entropy of ``train.py:126-136`` with
+  ``src/kernels/lmhead_xent.py:367-396``: logits = hidden W_embed^T accumulated in fp32, mean over the
+  non-ignored targets (the fused kernel's chunking over the vocabulary does not change the value).
+* ``trapezoidal`` follows ``src/kernels/trapezoidal.py:1-52``; ``rope`` follows ``src/kernels/rope.py:1-25``;
+  ``rmsnorm`` follows ``src/kernels/rmsnorm.py:222-235`` (fp32 statistics, output in the input dtype).
 
 The SSD function is a parameter with the reference's public signature
 ``ssd(x, A, B, C, chunk_size, initial_states=None, cache=None) -> (Y, final_state, cache)``, so the same model
@@ -23,6 +29,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+import torch.utils.checkpoint
 
 
 def rmsnorm(x, weight, eps=1e-6):
@@ -121,12 +128,12 @@ class SwiGLU(nn.Module):
 
 
 class Layer(nn.Module):
-    def __init__(self, ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden):
+    def __init__(self, ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden=None, dtype=torch.bfloat16):
         super().__init__()
-        self.norm1 = RMSNorm(d_model)
-        self.mixer = Mamba3Block(ssd, d_model, d_state, expand, n_heads, chunk_size)
-        self.norm2 = RMSNorm(d_model)
-        self.mlp = SwiGLU(d_model, mlp_hidden)
+        self.norm1 = RMSNorm(d_model, eps=1e-5)
+        self.mixer = Mamba3Block(ssd, d_model, d_state, expand, n_heads, chunk_size, dtype=dtype)
+        self.norm2 = RMSNorm(d_model, eps=1e-5)
+        self.mlp = SwiGLU(d_model, mlp_hidden or int(d_model * 2.5), dtype=dtype)
 
     def forward(self, h):
         h = h + self.mixer(self.norm1(h))
@@ -134,20 +141,30 @@ class Layer(nn.Module):
 
 
 class Mamba3LM(nn.Module):
-    def __init__(self, ssd, vocab, d_model, n_layers, d_state, expand, n_heads, chunk_size, mlp_hidden):
-        super().__init__()
-        self.embed = nn.Embedding(vocab, d_model, dtype=torch.bfloat16)
-        self.layers = nn.ModuleList(
-            [Layer(ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden) for _ in range(n_layers)])
-        self.norm_f = RMSNorm(d_model)
-        self.lm_head = nn.Linear(d_model, vocab, bias=False, dtype=torch.bfloat16)
+    """Embedding, ``n_layers`` layers, final RMSNorm, LM head tied to the embedding. ``checkpoint``
+    recomputes each layer's forward in the backward (both SSD variants alike), bounding the memory of a
+    24-layer step."""
 
-    def loss(self, tokens, targets):
+    def __init__(self, ssd, vocab, d_model, n_layers, d_state, expand, n_heads, chunk_size, mlp_hidden=None,
+                 dtype=torch.bfloat16, checkpoint=False):
+        super().__init__()
+        self.embed = nn.Embedding(vocab, d_model, dtype=dtype)
+        nn.init.normal_(self.embed.weight, std=1.0 / d_model ** 0.5)
+        self.layers = nn.ModuleList(
+            [Layer(ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden, dtype) for _ in range(n_layers)])
+        self.norm_f = RMSNorm(d_model, eps=1e-5)
+        self.checkpoint = checkpoint
+
+    def loss(self, tokens, targets, ignore_index=-100):
         h = self.embed(tokens)
         for layer in self.layers:
-            h = layer(h)
-        logits = self.lm_head(self.norm_f(h))
-        return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), targets.reshape(-1))
+            if self.checkpoint:
+                h = torch.utils.checkpoint.checkpoint(layer, h, use_reentrant=False)
+            else:
+                h = layer(h)
+        hidden = self.norm_f(h)
+        logits = hidden.float() @ self.embed.weight.float().t()
+        return F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1), ignore_index=ignore_index)
 
 
 def set_ssd(model, ssd):

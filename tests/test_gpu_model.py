@@ -1,23 +1,26 @@
-"""Model-level parity, BASELINE config 4's check at a reduced size: one training step (loss and every
-parameter's gradient) of a Mamba-3-style LM (tests/model_lib.py) with the native SSD swapped in, against the
-same model, weights and tokens with the oracle's restatement of the reference SSD. Two sizes: two small layers
-on a sequence that is not a chunk multiple, and one layer at config 4's exact layer shape.
+"""Model-level parity: one training step (loss and every parameter's gradient) of a
+Mamba-3-style LM (tests/model_lib.py) with the native SSD swapped in, against the same model, weights and
+tokens with the oracle's restatement of the reference SSD.
 
-Both runs share every op outside the SSD (bf16 weights and activations, as the reference block runs), so the
-differences come from the SSD alone: the native kernel computes in bf16 with fp32 accumulation, the oracle in
-fp32 on the same bf16 values, its outputs rounded back to bf16 at the block's boundary. The blocks make the
-reference's two SSD calls per layer (the beta path reusing the gamma path's cache, which drops the beta
-path's A gradient in both) on a sequence that is not a chunk multiple, so they also pad as the reference does.
+* Config 4 at its stated size: 24 layers, d_model 1024, expand 2 (H = 32, P = 64), N = 128 per-head B/C,
+  vocab 50 304, B = 4, L = 4096, tied LM head with fp32 cross-entropy.
+  - fp32: the whole model in fp32, the native SSD in fp32 against the oracle in fp32. Loss within 1e-4
+    relative, every parameter's gradient within 1e-3 normwise (max|d| / max|ref|).
+  - bf16: the model in bf16 as the reference trains it, the native SSD in bf16 against the oracle in fp32
+    on the same bf16 values. A model-level gradient sums the whole step's products and bf16 rounding inside
+    the SSD moves it by more than the per-op 1e-2; the reference's own bf16 arithmetic (the oracle with every
+    intermediate and its gradient stored in bf16, fp32 inside each contraction) sets the scale. Over the
+    step's gradients, the median of (native deviation / reference bf16 deviation) must stay within 1.5 and
+    its 90th percentile within 2.5, and each tensor within three times the reference's deviation (two
+    independent draws of rounding noise) or 2e-2. At 24 layers some gradients (dt_bias, A_log of deep layers)
+    are dominated by that noise in both runs: both deviate from the fp32 math by more than 50 %.
+* Config 4's layer shape with one layer, and a two-layer composition on a padded sequence (T not a chunk
+  multiple), both bf16 with the same criterion.
 
-Tolerances (normwise, max|got - ref| / max|ref| per tensor): the loss to 1e-3. A model-level gradient sums the
-whole step's products, and bf16 rounding inside the SSD moves it by several times the per-op 1e-2 bound: the
-reference itself, run with bf16 intermediates as it does on bf16 inputs (the oracle in bf16), deviates from the
-fp32 math by up to about 8e-2 on the in-projection gradient of the small model, and by up to 0.37 at config 4's
-layer shape, where the RoPE angles accumulate over 4096 tokens and bf16 rounding of the SSD's inputs and outputs
-is amplified through them. So each native gradient must stay within twice the reference's own bf16 deviation for
-that tensor, and never needs to beat 2e-2. The SSD-facing gradients (A_log, D, the B/C biases and norms) stay
-within 1.3e-2 at config 4's shape. On the CPU the check fails for a dropped dA gradient and for a beta call that
-ignores the cache (A_log off by 0.5-1.0).
+Every op outside the SSD is shared by the runs (same weights, same ops), so the differences come from the SSD
+alone. The blocks make the reference's two SSD calls per layer (the beta path reusing the gamma path's cache,
+which drops the beta path's A gradient in both). Layers are checkpointed (recomputed in the backward) in every
+run alike. On the CPU the check fails for a dropped dA gradient and for a beta call that ignores the cache.
 """
 from __future__ import annotations
 
@@ -33,58 +36,91 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not gpu_available(), reason="needs an MI355X (HIP device)")]
 
 DEV = "cuda"
-SIZES = dict(vocab=512, d_model=256, n_layers=2, d_state=128, expand=2, n_heads=8, chunk_size=256,
-             mlp_hidden=512)
-LOSS_TOL, GRAD_FLOOR, GRAD_FACTOR = 1e-3, 2e-2, 2.0
+CONFIG4 = dict(vocab=50304, d_model=1024, n_layers=24, d_state=128, expand=2, n_heads=32, chunk_size=256)
+CONFIG4_BT = (4, 4096)
+SMALL = dict(vocab=512, d_model=256, n_layers=2, d_state=128, expand=2, n_heads=8, chunk_size=256)
+CONFIG4_LAYER = dict(CONFIG4, n_layers=1)
 
 
 def reference_ssd(x, A, B, C, chunk_size, initial_states=None, cache=None):
-    """The oracle's reference SSD in fp32 on the block's bf16 values; Y back in the block's dtype."""
+    """The oracle's reference SSD in fp32 on the block's values; Y back in the block's dtype."""
     Y, final, out_cache = oc.fused_ssd_scan(x.float(), A.float(), B.float(), C.float(), chunk_size,
                                             initial_states, cache)
     return Y.to(x.dtype), final, out_cache
 
 
-def reference_ssd_bf16(x, A, B, C, chunk_size, initial_states=None, cache=None):
-    """The oracle's reference SSD in the inputs' dtype (bf16 intermediates, as the reference runs)."""
-    return oc.fused_ssd_scan(x, A, B, C, chunk_size, initial_states, cache)
+def reference_ssd_bf16_storage(x, A, B, C, chunk_size, initial_states=None, cache=None):
+    """The reference's arithmetic on bf16 inputs: bf16 tensors between its ops, fp32 inside each
+    contraction (oracle storage emulation; fp32 math, so no bf16 batched products run)."""
+    Y, final, out_cache = oc.fused_ssd_scan(x.float(), A.float(), B.float(), C.float(), chunk_size,
+                                            initial_states, cache, storage=torch.bfloat16)
+    return Y.to(x.dtype), final, out_cache
 
 
-def _step(model, tokens, targets):
+def _step(model, tokens, targets, tag):
     model.zero_grad(set_to_none=True)
     loss = model.loss(tokens, targets)
     loss.backward()
+    torch.cuda.synchronize()
+    print(f"  {tag}: loss {loss.item():.6f}", flush=True)
     return loss.detach().double().item(), {n: p.grad.detach().clone() for n, p in model.named_parameters()}
 
 
-# config 4's layer: d_model 1024, expand 2 (H = 32, P = 64), N = 128, per-head B/C, B = 4, L = 4096; one layer
-# and a small vocabulary (the LM head is not what is checked)
-SIZES_CFG4_LAYER = dict(vocab=2048, d_model=1024, n_layers=1, d_state=128, expand=2, n_heads=32, chunk_size=256,
-                        mlp_hidden=2048)
-
-
-@pytest.mark.parametrize("sizes,b,T", [(SIZES, 2, 384), (SIZES_CFG4_LAYER, 4, 4096)],
-                         ids=["small_two_layers_padded", "config4_layer_shape"])
-def test_mamba3_lm_training_step_native_ssd_matches_reference_ssd(sizes, b, T):
+def _model_and_batch(sizes, b, T, dtype, checkpoint):
     import kernels
     torch.manual_seed(0)
-    model = Mamba3LM(kernels.fused_ssd_scan, **sizes).to(DEV)
+    model = Mamba3LM(kernels.fused_ssd_scan, **sizes, dtype=dtype, checkpoint=checkpoint).to(DEV)
     g = torch.Generator().manual_seed(1)
     tokens = torch.randint(0, sizes["vocab"], (b, T), generator=g).to(DEV)
     targets = torch.randint(0, sizes["vocab"], (b, T), generator=g).to(DEV)
+    return model, tokens, targets
 
-    loss_n, grads_n = _step(model, tokens, targets)
+
+def test_config4_training_step_fp32():
+    """24 layers at config 4's shape in fp32: loss to 1e-4 relative, every gradient to 1e-3 normwise."""
+    import kernels
+    model, tokens, targets = _model_and_batch(CONFIG4, *CONFIG4_BT, torch.float32, checkpoint=True)
+    loss_n, grads_n = _step(model, tokens, targets, "native fp32 SSD")
     set_ssd(model, reference_ssd)
-    loss_r, grads_r = _step(model, tokens, targets)
-    set_ssd(model, reference_ssd_bf16)
-    _, grads_b = _step(model, tokens, targets)
-
-    print(f"loss native {loss_n:.6f} reference {loss_r:.6f}", flush=True)
-    assert abs(loss_n - loss_r) <= LOSS_TOL * abs(loss_r), (loss_n, loss_r)
-    assert grads_n.keys() == grads_r.keys() == grads_b.keys()
+    loss_r, grads_r = _step(model, tokens, targets, "oracle fp32 SSD")
+    assert abs(loss_n - loss_r) <= 1e-4 * abs(loss_r), (loss_n, loss_r)
+    assert grads_n.keys() == grads_r.keys()
+    worst = ("", 0.0)
     for name, gr in grads_r.items():
         assert gr.abs().max().item() > 0, f"{name}: zero reference gradient"
         e = rel_err(grads_n[name], gr)
-        bound = max(GRAD_FLOOR, GRAD_FACTOR * rel_err(grads_b[name], gr))
-        print(f"{name:40s} {e:.3e} (bound {bound:.3e})", flush=True)
+        worst = max(worst, (name, e), key=lambda t: t[1])
+        assert e <= 1e-3, f"{name}: rel err {e:.3e} > 1e-3"
+    print(f"  {len(grads_r)} gradients, worst {worst[0]} {worst[1]:.2e}", flush=True)
+    set_ssd(model, kernels.fused_ssd_scan)
+
+
+@pytest.mark.parametrize("sizes,b,T,checkpoint", [(SMALL, 2, 384, False), (CONFIG4_LAYER, *CONFIG4_BT, False),
+                                                   (CONFIG4, *CONFIG4_BT, True)],
+                         ids=["small_two_layers_padded", "config4_one_layer", "config4_24_layers"])
+def test_training_step_bf16(sizes, b, T, checkpoint):
+    model, tokens, targets = _model_and_batch(sizes, b, T, torch.bfloat16, checkpoint)
+    loss_n, grads_n = _step(model, tokens, targets, "native bf16 SSD")
+    set_ssd(model, reference_ssd)
+    loss_r, grads_r = _step(model, tokens, targets, "oracle fp32 SSD on bf16 values")
+    set_ssd(model, reference_ssd_bf16_storage)
+    loss_b, grads_b = _step(model, tokens, targets, "oracle, bf16 storage")
+    assert grads_n.keys() == grads_r.keys() == grads_b.keys()
+    rows = []
+    for name, gr in grads_r.items():
+        assert gr.abs().max().item() > 0, f"{name}: zero reference gradient"
+        e, eb = rel_err(grads_n[name], gr), rel_err(grads_b[name], gr)
+        rows.append((e / max(eb, 1e-12), name, e, eb))
+    rows.sort(reverse=True)
+    ratios = sorted(r[0] for r in rows)
+    print(f"  {len(rows)} gradients; native / reference-bf16 deviation: median {ratios[len(ratios) // 2]:.2f}, "
+          f"90th pct {ratios[int(0.9 * len(ratios))]:.2f}, max {ratios[-1]:.2f}", flush=True)
+    for r, name, e, eb in rows[:8]:
+        print(f"    {name:40s} native {e:.2e} reference-bf16 {eb:.2e} ratio {r:.2f}", flush=True)
+    assert abs(loss_n - loss_r) <= 1e-3 * abs(loss_r), (loss_n, loss_r)
+    # the native SSD's bf16 arithmetic moves the gradients as much as the reference's own does ...
+    assert ratios[len(ratios) // 2] <= 1.5 and ratios[int(0.9 * len(ratios))] <= 2.5, ratios
+    # ... and no tensor by more than three times as much (two independent rounding-noise draws)
+    for r, name, e, eb in rows:
+        bound = max(2e-2, 3.0 * eb)
         assert e <= bound, f"{name}: rel err {e:.3e} > {bound:.3e}"

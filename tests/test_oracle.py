@@ -346,3 +346,31 @@ def test_extended_gated_norm_backward_matches_reference_closed_form():
     assert torch.allclose(dy, dy_ref, atol=1e-12)
     assert torch.allclose(dw, dw_ref, atol=1e-12)
     assert torch.allclose(dz, dz_ref, atol=1e-12)
+
+
+def test_storage_emulation_of_the_bf16_reference_run():
+    """fused_ssd_scan(storage=bf16) on wide inputs: fp32 arithmetic with every intermediate (and its gradient)
+    rounded to bf16. It must be the plain oracle when storage is the inputs' own dtype, move the results by a
+    bf16-sized amount, and land within a small factor of an actual bf16 run of the oracle (CPU bf16 einsum,
+    fp32 accumulation inside each contraction)."""
+    x, A, B, C = make_reference_test_inputs(2, 256, 4, 16, 8, seed=5)
+    x, A, B, C = [t.bfloat16().double() for t in (x, A, B, C)]
+    dY = torch.randn(2, 256, 4, 16, generator=torch.Generator().manual_seed(6)).bfloat16().double()
+
+    def run(dtype, storage):
+        leaves = [t.detach().clone().to(dtype).requires_grad_(True) for t in (x, A, B, C)]
+        Y, fin, _ = oc.fused_ssd_scan(*leaves, 64, storage=storage)
+        Y.backward(dY.to(dtype))
+        return [Y.detach().double()] + [t.grad.double() for t in leaves]
+
+    ref = run(torch.float64, None)
+    same = run(torch.float64, torch.float64)
+    emu = run(torch.float32, torch.bfloat16)
+    real = run(torch.bfloat16, None)
+    rel = lambda a, b: ((a - b).abs().max() / b.abs().max()).item()  # noqa: E731
+    for r, s_ in zip(ref, same):
+        assert torch.equal(r, s_)
+    for name, r, e, b in zip(("Y", "dx", "dA", "dB", "dC"), ref, emu, real):
+        de, db = rel(e, r), rel(b, r)
+        assert 1e-4 < de < 5e-2, (name, de)
+        assert de < 4 * db + 1e-3 and db < 4 * de + 1e-3, (name, de, db)
