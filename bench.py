@@ -253,6 +253,81 @@ def time_gpu(steps, warmup, probe=False):
     return ms_total / steps, wall / steps * 1e3, phases, nchunks
 
 
+TRAPZ_LAYER = dict(batch=4, seqlen=4096, nheads=32, headdim=64, ngroups=32, dstate=128, chunk=256)
+
+
+def time_trapezoidal(steps=10, warmup=3):
+    """The trapezoidal block's SSD section at config 4's layer shape (mamba_base_engine.py:167-191),
+    fwd+bwd per step, bf16: one reference-API SSD call alone (fused_ssd_scan on x*gamma), the block's
+    two calls as the reference composes them (gamma call, shift, beta call reusing the cache, sum,
+    + D x, gated RMSNorm; torch glue), and the fused single-scan op with the same D and norm in both
+    gradient settings. Inputs from the trapezoidal producer (gamma = lam dt, beta = (1-lam) dt e^dA)."""
+    import torch
+    import torch.nn.functional as F
+    import kernels
+
+    dev = torch.device("cuda", 0)
+    b, L, H, P, G, N, Q = (TRAPZ_LAYER[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate",
+                                                       "chunk"))
+    g = torch.Generator(device=dev).manual_seed(5)
+    kw = dict(generator=g, device=dev, dtype=torch.float32)
+    bf = torch.bfloat16
+    dt = F.softplus(torch.randn(b, L, H, **kw) - 1.0)
+    A = -torch.exp(torch.rand(H, **kw) * 3.0 - 4.0)
+    lam = torch.sigmoid(torch.randn(b, L, H, **kw))
+    dA = dt * A
+    t = {"x": torch.randn(b, L, H, P, **kw).to(bf), "dA": dA.to(bf), "gamma": (lam * dt).to(bf),
+         "beta": ((1 - lam) * dt * torch.exp(dA)).to(bf), "B": torch.randn(b, L, G, N, **kw).to(bf),
+         "C": torch.randn(b, L, G, N, **kw).to(bf), "D": torch.randn(H, **kw),
+         "z": torch.randn(b, L, H, P, **kw).to(bf),
+         "w": torch.ones(H * P, device=dev), "dy": torch.randn(b, L, H, P, **kw).to(bf)}
+    leaves = {k: v.clone().requires_grad_(True) for k, v in t.items() if k != "dy"}
+    xg = (t["x"] * t["gamma"].unsqueeze(-1)).requires_grad_(True)
+
+    def one_call():
+        y, _, _ = kernels.fused_ssd_scan(xg, leaves["dA"], leaves["B"], leaves["C"], Q)
+        y.backward(t["dy"])
+
+    def shift(v):
+        return F.pad(v[:, :-1], (0, 0) * (v.dim() - 2) + (1, 0))
+
+    def two_calls():
+        l = leaves
+        y_g, _, cache = kernels.fused_ssd_scan(l["x"] * l["gamma"].unsqueeze(-1), l["dA"], l["B"], l["C"], Q)
+        y_b, _, _ = kernels.fused_ssd_scan(shift(l["x"]) * l["beta"].unsqueeze(-1), l["dA"], shift(l["B"]), l["C"], Q,
+                                           cache=cache)
+        y = (y_g + y_b + l["x"] * l["D"].to(bf).view(1, 1, -1, 1)).reshape(b, L, H * P).float()
+        y = (y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + 1e-6) * l["w"]).to(bf) * F.silu(l["z"].reshape(b, L, -1))
+        y.backward(t["dy"].reshape(b, L, -1))
+
+    def fused(exact):
+        l = leaves
+        y = kernels.fused_trapezoidal_ssd_scan(l["x"], l["dA"], l["gamma"], l["beta"], l["B"], l["C"], Q, D=l["D"],
+                                               z=l["z"], norm_weight=l["w"], exact_beta_dA=exact)
+        y.backward(t["dy"])
+
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, fn in (("one_ssd_call_ms", one_call), ("two_calls_ms", two_calls),
+                     ("fused_drop_beta_dA_ms", lambda: fused(False)), ("fused_exact_dA_ms", lambda: fused(True))):
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) / steps, 4)
+    one = res["one_ssd_call_ms"]
+    return {"workload": "config 4 layer: B=4 L=4096 H=32 P=64, per-head B/C N=128, chunk 256, bf16; "
+                        "fwd+bwd; two calls and fused with + D x and the gated RMSNorm",
+            **res, "fused_drop_over_one_call": round(res["fused_drop_beta_dA_ms"] / one, 3),
+            "fused_exact_over_one_call": round(res["fused_exact_dA_ms"] / one, 3),
+            "fused_drop_over_two_calls": round(res["fused_drop_beta_dA_ms"] / res["two_calls_ms"], 3)}
+
+
 def kernel_roofline(name, ms, models):
     """Roofline entry of one phase: HBM-bound below the ridge, MFMA-bound above."""
     flops, nbytes = models.get(name, (0, 0))
@@ -346,6 +421,8 @@ def main():
                     help="run one plain 1 GiB device copy first (counter calibration)")
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS),
                     help="BASELINE config to time (2 = the headline shape)")
+    ap.add_argument("--no-trapezoidal", action="store_true",
+                    help="skip the trapezoidal block line (config 4's layer, two calls vs the fused op)")
     a = ap.parse_args()
     global CFG, CFG_ID
     CFG, CFG_ID = dict(CONFIGS[a.config]), a.config
@@ -370,6 +447,8 @@ def main():
         "kernels_roofline": per_kernel,
         "wall_ms_per_step": wall_ms,
     }
+    if rank == 0 and not a.no_trapezoidal and CFG_ID == 2:
+        out["trapezoidal_block"] = time_trapezoidal()
     if rank == 0 and not a.no_cpu_baseline and CFG_ID == 2:
         out["cpu_baseline"] = cpu_baseline()
     if rank == 0:

@@ -45,7 +45,8 @@ __device__ __forceinline__ void ld_per(const float* __restrict__ p, float (&o)[P
 template <typename T, int PER>
 __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const ChunkInfo* __restrict__ chunks,
                                                     const float* __restrict__ Ah, const float* __restrict__ dt,
-                                                    float* __restrict__ ddt, T* __restrict__ dA_tok) {
+                                                    float* __restrict__ ddt, T* __restrict__ dA_tok,
+                                                    float* __restrict__ da32) {
   // dt / ddt of the block's four heads are 16 contiguous bytes per position when H % 4 == 0: then
   // thread t moves position t's four values with one 16-byte access through LDS (the per-head
   // 4-byte accesses touch a line per lane, four times as many L2 requests)
@@ -136,7 +137,7 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
   }
   const float excl = incl - run;
   float dAp = 0.0f;
-  if (d.a_mode == 0 && ddt && d.has_dt) ld_per<PER>(bf.xdx + base + l0, t);
+  if (ddt && d.has_dt) ld_per<PER>(bf.xdx + base + l0, t);
 #pragma unroll
   for (int e = 0; e < per; ++e) {
     const int l = l0 + e;
@@ -149,7 +150,10 @@ __global__ void __launch_bounds__(256) k_bwd_finish(SsdDims d, SsdBufs bf, const
       else if (ddt && d.has_dt) ddt[row * d.H + h] = t[e] + Ah[h] * da;
       dAp += dtv * da;
     } else {
+      // per-token decay (with dt: the trapezoidal mode's scan, where a does not depend on dt)
       if (dA_tok) dA_tok[row * d.H + h] = from_f<T>(da);
+      if (da32) da32[row * d.H + h] = da;
+      if (ddt && d.has_dt) ddt[row * d.H + h] = t[e];
     }
   }
   for (int o = 32; o > 0; o >>= 1) dAp += __shfl_xor(dAp, o, 64);
@@ -187,24 +191,24 @@ size_t lds_bwd_row(int dtype, const SsdDims& d) {
 
 template <int PER>
 static void bwd_finish_launch(int dtype, dim3 grid, const SsdDims& d, const SsdBufs& b, const float* Ah,
-                              const float* dt, float* ddt, void* dA_tok, hipStream_t s) {
+                              const float* dt, float* ddt, void* dA_tok, float* da32, hipStream_t s) {
   if (dtype == 1)
     hipLaunchKernelGGL((k_bwd_finish<bf16, PER>), grid, dim3(256), 0, s, d, b, b.chunks, Ah, dt, ddt,
-                       reinterpret_cast<bf16*>(dA_tok));
+                       reinterpret_cast<bf16*>(dA_tok), da32);
   else
     hipLaunchKernelGGL((k_bwd_finish<float, PER>), grid, dim3(256), 0, s, d, b, b.chunks, Ah, dt, ddt,
-                       reinterpret_cast<float*>(dA_tok));
+                       reinterpret_cast<float*>(dA_tok), da32);
 }
 
 hipError_t launch_bwd_finish(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in, float* ddt,
-                             void* dA_tok, hipStream_t s) {
+                             void* dA_tok, float* da32, hipStream_t s) {
   dim3 grid(d.max_chunks, (d.H + 3) / 4);
   const float* Ah = d.a_mode == 0 ? reinterpret_cast<const float*>(in.A) : nullptr;
   switch (d.Qpad / 64) {
-    case 1: bwd_finish_launch<1>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
-    case 2: bwd_finish_launch<2>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
-    case 3: bwd_finish_launch<3>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s); break;
-    default: bwd_finish_launch<4>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, s);
+    case 1: bwd_finish_launch<1>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, da32, s); break;
+    case 2: bwd_finish_launch<2>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, da32, s); break;
+    case 3: bwd_finish_launch<3>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, da32, s); break;
+    default: bwd_finish_launch<4>(dtype, grid, d, b, Ah, in.dt, ddt, dA_tok, da32, s);
   }
   return hipGetLastError();
 }

@@ -57,6 +57,7 @@ struct BwdFactArgs {
   float* xdx;
   float* dD_part;  // [MC][H][Qpad/64]
   float* dS;       // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
+  const float* Dtok;   // trapezoidal mode: D per token, [R][H]
   int nslices, hslice;
 };
 
@@ -153,13 +154,15 @@ struct BwdFactScalars {
   float fcs;        // cs at row 64 j + (staging thread index): the head's f_l
   float ecs, edt;   // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
   float cj, cl;     // cs at the last token of block j and of the chunk
-  float D;          // the head's D (0 without D)
+  float D;          // the head's D (0 without D); trapezoidal mode: D at that token
   int fast;
 };
 
 }  // namespace
 
-template <int PT, int NT>
+// MODE: 0 plain, 1 trapezoidal (strictly causal S, D per token), 2 decay gradient only (no dx, no
+// dS tiles); compile-time so that the plain kernel carries none of the others' code
+template <int PT, int NT, int MODE>
 __global__ void __launch_bounds__(kThreads)
 k_bwd_fact(SsdDims d, BwdFactArgs a) {
   using LD = BwdFactLds<PT, NT>;
@@ -237,10 +240,11 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         }
 #pragma unroll
         for (int kk = 0; kk < NP / 16; ++kk) mfma(Sq, tld8<NP>(Bt, 32 * wr + l32, 16 * kk + 8 * hh), cb[kk]);
-        if (t == 0) {  // diagonal tile: s > l is outside the causal mask
+        if (t == 0) {  // diagonal tile: s > l is outside the causal mask (s >= l in trapezoidal mode)
+          constexpr int sd = MODE == 1 ? 1 : 0;
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            if (32 * wr + acc_row(v, lane) > 32 * wc + l32) Sq[v] = 0.0f;
+            if (32 * wr + acc_row(v, lane) + sd > 32 * wc + l32) Sq[v] = 0.0f;
         }
       }
       ur_set(UR + 4 * uu, Sq);  // dS (entries 4 (kNsw + u) ..) starts at zero
@@ -278,7 +282,11 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     hs.ecs = buf_ldf(rcs, tok * 4, true);
     hs.edt = buf_ldf(rdt, tok * d.H * 4, d.has_dt && tok < ci.len);
     hs.cl = buf_ldf(rcs, (Qpad - 1) * 4, true);
-    hs.D = buf_ldf(buf_rsrc(d.has_D ? a.Dv : csh), h * 4, d.has_D);
+    // D of the head, or (trapezoidal mode) of the head at that token
+    if constexpr (MODE == 1)
+      hs.D = buf_ldf(buf_rsrc(a.Dtok + (int64_t)ci.row0 * d.H + h), tok * d.H * 4, tok < ci.len);
+    else
+      hs.D = buf_ldf(buf_rsrc(d.has_D ? a.Dv : csh), h * 4, d.has_D);
     hs.cj = buf_ldf(rcs, (64 * j + 63) * 4, true);
     hs.fast = __float_as_int(buf_ldf(buf_rsrc(a.fast + (int64_t)c * d.H), h * 4, true));
     const int64_t xo = (int64_t)h * d.P;
@@ -318,7 +326,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
 #pragma unroll
     for (int id = threadIdx.x; id < 64 * CPR; id += kThreads) {
       const int r = id / CPR, k = (id % CPR) * 8;
-      if (64 * j + r < ci.len && k < d.P)
+      if (64 * j + r < ci.len && k < d.P && MODE != 2)
         *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + k) =
             tld8<PP>(ot, r, k);
     }
@@ -412,7 +420,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         zero(dXs);
 #pragma unroll
         for (int t = 0; t < kSlots; ++t) {
-          if (t >= nt_i) continue;
+          if (t >= nt_i || MODE == 2) continue;  // (the decay gradient needs the state term only)
           const bf16* dyt = dyr + t * XT;
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk)
@@ -465,7 +473,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   flush(head(nh - 1));
 
   // ---- dS tiles, summed over the slice's heads (zero outside the causal mask) ----
-  if (xrole) return;
+  if (xrole || MODE == 2) return;
   float* dSbase = a.dS + (((int64_t)slc * d.max_chunks + c) * d.G + g) * (int64_t)(nb * nb) * 4096;
 #pragma unroll
   for (int uu = 0; uu < kNsw; ++uu) {
@@ -479,7 +487,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int s_loc = 32 * wr + 8 * r + 4 * hh + e;
-        q[e] = (t == 0 && s_loc > l_loc) ? 0.0f : __uint_as_float(UR[4 * (kNsw + uu) + r][e]);
+        q[e] = (t == 0 && s_loc + (MODE == 1 ? 1 : 0) > l_loc) ? 0.0f : __uint_as_float(UR[4 * (kNsw + uu) + r][e]);
       }
       *reinterpret_cast<floatx4*>(tile + l_loc * 64 + 32 * wr + 8 * r + 4 * hh) = q;
     }
@@ -505,8 +513,16 @@ static hipError_t bwd_fact_t(const SsdDims& d, const BwdFactArgs& a, hipStream_t
   const int U = d.max_chunks * d.G * a.nslices;
   const int blocks = (U + 7) / 8 * 8 * (d.Qpad / 64);
   const size_t lds = BwdFactLds<PT, NT>::bytes(d.Qpad);
-  ensure_lds(k_bwd_fact<PT, NT>, lds);
-  hipLaunchKernelGGL((k_bwd_fact<PT, NT>), dim3(blocks), dim3(kThreads), lds, s, d, a);
+  if (d.da_only) {
+    ensure_lds(k_bwd_fact<PT, NT, 2>, lds);
+    hipLaunchKernelGGL((k_bwd_fact<PT, NT, 2>), dim3(blocks), dim3(kThreads), lds, s, d, a);
+  } else if (d.trapz) {
+    ensure_lds(k_bwd_fact<PT, NT, 1>, lds);
+    hipLaunchKernelGGL((k_bwd_fact<PT, NT, 1>), dim3(blocks), dim3(kThreads), lds, s, d, a);
+  } else {
+    ensure_lds(k_bwd_fact<PT, NT, 0>, lds);
+    hipLaunchKernelGGL((k_bwd_fact<PT, NT, 0>), dim3(blocks), dim3(kThreads), lds, s, d, a);
+  }
   return hipGetLastError();
 }
 
@@ -529,6 +545,7 @@ hipError_t launch_bwd_fact(const SsdDims& d, const SsdBufs& b, const SsdIn& in, 
   a.eterm = b.eterm;
   a.xdx = b.xdx;
   a.dD_part = b.dD_part;
+  a.Dtok = b.Dtok;
   a.dS = b.dS_tiles;
   a.nslices = b.nslices;
   a.hslice = b.hslice;

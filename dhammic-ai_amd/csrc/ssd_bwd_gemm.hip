@@ -49,7 +49,8 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
                                                   const float* __restrict__ dS, int nslices,
                                                   const float* __restrict__ dS_fix, const int32_t* __restrict__ fast,
                                                   float* __restrict__ dcs_off, bf16* __restrict__ dB,
-                                                  bf16* __restrict__ dC) {
+                                                  bf16* __restrict__ dC, const float* __restrict__ tz_gam,
+                                                  float* __restrict__ xdy) {
   using Cfg = GemmCfg<PT, NT>;
   constexpr int PP = Cfg::PP, NP = Cfg::NP, NTW = (NT + 1) / 2, NK = PP / 16;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -120,6 +121,9 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     if (w == 1) {
       rs = buf_rsrc(dt + (int64_t)(ci.row0 + 64 * kb) * d.H + h);
       off = lane < nrows && d.has_dt ? lane * d.H * 4 : SSD_BUF_SIZE;
+    } else if (w == 3 && d.trapz) {  // trapezoidal mode: gamma of the block's tokens
+      rs = buf_rsrc(tz_gam + (int64_t)(ci.row0 + 64 * kb) * d.H + h);
+      off = lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE;
     } else {
       rs = buf_rsrc(csh);
       off = w == 0 ? (64 * kb + lane) * 4 : (Qpad - 1) * 4;
@@ -127,6 +131,8 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)sc, 4, off, 0, 0, 0);
   };
 
+  // trapezoidal mode: sum_h gamma (x_t . dy_t), the diagonal of dS (dC waves)
+  float dcb = 0.0f;
   // dC (waves 0-3) or dB (waves 4-7) rows t, columns n of the wave's n tiles
   floatx16 acc[NTW];
 #pragma unroll
@@ -166,6 +172,7 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     lds_barrier();  // head k visible in LDS; slot (k + 2) % 3 is free (head k - 1 done)
     ring_step(smem + (k % 3) * Cfg::kSlot, smem + ((k + 2) % 3) * Cfg::kSlot, !brole && k + 2 < nhd,
               [&](unsigned char* nxt) { issue(head(k + 2), nxt); }, [&](const unsigned char* base) {
+    if (brole && d.da_only) return;  // decay gradient only: no dB
     lane = opaque_lane();
     hh = lane >> 5;
     l32 = lane & 31;
@@ -207,14 +214,34 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     if (!brole) {
       osum = add_xor32(osum);
       if (hh == 0 && tok) dcs_off[((int64_t)nh * MC * d.H + (int64_t)c * d.H + h) * Qpad + t] = osum * et * pt_;
+      if (d.trapz) {
+        // x_t . dy_t from the staged rows (rf holds dy_t), for dgamma and the diagonal of dS
+        float xd = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+          const bf16x8 xr = swz_nat8<PP>(tx, t_loc, 16 * kk + 8 * hh);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xd = fmaf((float)xr[e], (float)rf[kk][e], xd);
+        }
+        xd = add_xor32(xd);
+        if (nh == 0 && hh == 0 && tok) xdy[((int64_t)c * d.H + h) * Qpad + t] = xd;
+        dcb = fmaf(scal[192 + t_loc], xd, dcb);
+      }
     }
     });
   }
 
+  if (d.da_only) return;  // decay gradient only: the Y_off term above is all it needs
   // ---- tile terms: dC += dS[kb, j] B_j (j <= kb), dB += dS[i, kb]^T C_i (i >= kb) ----
   constexpr int PI = tpitch_tr<NP>();
   bf16* tBC = reinterpret_cast<bf16*>(smem);         // [64][NP], padded
   bf16* tS = tBC + tsize<64, NP, PI>();              // [64][64] bf16, padded
+  float* s_dcb = reinterpret_cast<float*>(smem + Cfg::bytes) - 64;  // [64] (trapezoidal mode), past tS
+  static_assert(2 * (tsize<64, NP, PI>() + tsize<64, 64, tpitch<64>()>()) + 256 <= Cfg::bytes, "s_dcb");
+  if (d.trapz) {
+    __syncthreads();  // the ring's last reads are done
+    if (!brole && nh == 0 && hh == 0) s_dcb[t_loc] = dcb;
+  }
   const int nb = Qpad / 64;
   const int nbl = (ci.len + 63) >> 6;
   const int64_t sstride = (int64_t)MC * d.G * nb * nb * 4096;
@@ -243,6 +270,13 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
           const float* fx = dSf + (ti * nb + tj) * 4096;
           s0 += *reinterpret_cast<const floatx4*>(fx + r * 64 + k);
           s1 += *reinterpret_cast<const floatx4*>(fx + r * 64 + k + 4);
+        }
+        // trapezoidal mode: the scan is strictly causal and the diagonal term is the per-token
+        // D part gamma (C_t . B_t) x_t, so the diagonal of dS is sum_h gamma (x_t . dy_t)
+        if (d.trapz && ti == tj && (r >> 3) == (id & 7)) {
+          const float dg = s_dcb[r];  // tile (kb, kb): row r is token 64 kb + r
+          const int e = r & 7;
+          if (e < 4) s0[e] += dg; else s1[e - 4] += dg;
         }
         bf16x8 v;
         v[0] = (bf16)s0[0]; v[1] = (bf16)s0[1]; v[2] = (bf16)s0[2]; v[3] = (bf16)s0[3];
@@ -318,7 +352,7 @@ static hipError_t bwd_gemm_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in
                      reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(b.hin), b.dst16,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), b.dS_tiles,
                      b.nslices, b.dS_fix, b.fast, b.dcs_off, reinterpret_cast<bf16*>(dB),
-                     reinterpret_cast<bf16*>(dC));
+                     reinterpret_cast<bf16*>(dC), b.tz_gam, b.xdy);
   return hipGetLastError();
 }
 

@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(256) k_bwd_col(SsdDims d, SsdBufs bf, BwdCommo
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int l = r0 + wr * 32 + acc_row(v, lane);
-        const bool ok = s <= l && l < ci.len;
+        const bool ok = s + (d.trapz ? 1 : 0) <= l && l < ci.len;  // trapezoidal mode: strictly causal
         const float dd = csl[v] - cs_s;
         const float Lv = ok ? exp_clamp(dd) : 0.0f;
         const float m = sacc[v] * Lv;
@@ -239,7 +239,8 @@ __global__ void __launch_bounds__(256) k_bwd_col(SsdDims d, SsdBufs bf, BwdCommo
           if (sg < ci.len && p < d.P) {
             const int64_t o = (int64_t)(ci.row0 + sg) * xrow + (int64_t)h * d.P + p;
             const float dyv = to_f(in.dy[o]);
-            dx[o] = from_f<T>(dts * dX + Dh * dyv);
+            const float Dl = d.trapz ? bf.Dtok[(int64_t)(ci.row0 + sg) * d.H + h] : Dh;
+            dx[o] = from_f<T>(dts * dX + Dl * dyv);
             dpart += xv * dyv;
           }
         }
@@ -383,7 +384,7 @@ __global__ void __launch_bounds__(256) k_bwd_row(SsdDims d, SsdBufs bf, BwdCommo
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int sg = s0 + wr * 32 + acc_row(v, lane);
-        const bool ok = sg <= l_me && l_ok;
+        const bool ok = sg + (d.trapz ? 1 : 0) <= l_me && l_ok;
         const float dd = cs_l - css[v];
         const float Lv = ok ? exp_clamp(dd) : 0.0f;
         const float dsv = mt[v] * dts[v] * Lv;

@@ -45,6 +45,7 @@ struct BwdMainArgs {
   float* xdx;
   float* dD_part;     // [MC][H][Qpad/64]
   float* dS;          // [nslices][MC][G][nb*nb][64][64], tile (i, j) row-major [l][s]
+  const float* Dtok;  // trapezoidal mode: D per token, [R][H]
   int nslices, hslice;
   // fixup mode (non-null): only the heads flagged 0 here run (the factorised kernel
   // cannot take them); the block skips the others and exits if it has none
@@ -219,7 +220,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
     tstage_load_v(sd, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
 
     const float cs_last = s_cs2[Qpad - 1];
-    const float Dh = d.has_D ? a.Dv[h] : 0.0f;
+    const float Dh = d.trapz ? (t_ok ? a.Dtok[(int64_t)(ci.row0 + tg) * d.H + h] : 0.0f) : (d.has_D ? a.Dv[h] : 0.0f);
 
     float colacc[16];
 #pragma unroll
@@ -252,7 +253,7 @@ k_bwd_main(SsdDims d, BwdMainArgs a) {
         const int s_loc = 32 * wr + acc_row(v, lane);
         const float dd = cs_l - cs_s[v];
         float Lv = exp2_fast(clamp_med3(dd, -SSD_T2, SSD_T2));
-        if (diag && s_loc > l_loc) Lv = 0.0f;
+        if (diag && s_loc + (d.trapz ? 1 : 0) > l_loc) Lv = 0.0f;  // trapezoidal mode: strictly causal
         const float dmv = dm[v] * dt_s[v];
         const float M = (float)S[t][v >> 3][v & 7] * Lv;
         dS[t][v] = fmaf(dmv, Lv, dS[t][v]);
@@ -454,6 +455,7 @@ static BwdMainArgs make_main_args(const SsdDims& d, const SsdBufs& b, const SsdI
   a.eterm = b.eterm;
   a.xdx = b.xdx;
   a.dD_part = b.dD_part;
+  a.Dtok = b.Dtok;
   a.dS = fixup ? b.dS_fix : b.dS_tiles;
   a.nslices = fixup ? 1 : b.nslices;
   a.hslice = fixup ? d.hpg : b.hslice;

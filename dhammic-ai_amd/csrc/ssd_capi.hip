@@ -23,10 +23,11 @@ struct Plan {
   int dtype, state_dtype;
   int64_t nslices, hslice, npass_blk, norm_blocks;
   // byte offsets inside each workspace
-  size_t o_chunks, o_seq0, o_cs, o_fast, o_hin, o_ypre, o_rstd, saved_bytes;
+  size_t o_chunks, o_seq0, o_cs, o_fast, o_hin, o_ypre, o_rstd, o_tzdt, o_tzrho, o_tzgam, o_tzcb, o_Dtok, o_hgam,
+      saved_bytes;
   size_t o_st, fwd_bytes;
   size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dSf, o_dst16,
-      bwd_bytes;
+      o_xdy, o_tzddt, o_tzda, bwd_bytes;
   int fused_bwd, nrowg;
 };
 
@@ -49,6 +50,12 @@ int plan(const ssd_desc_t* s, Plan* p) {
   if (s->dA_skip & ~(SSD_DA_SKIP_INTRA | SSD_DA_SKIP_CUMSUM | SSD_DA_SKIP_CHUNK)) return SSD_ERR_INVALID;
   // a cached A_cumsum carries no gradient, and neither does the decay_chunk built from it
   if (s->a_mode == SSD_A_CUMSUM && (~s->dA_skip & (SSD_DA_SKIP_CUMSUM | SSD_DA_SKIP_CHUNK))) return SSD_ERR_INVALID;
+  // trapezoidal mode: per-token decay; dt, the initial / final state and the cache options are not part of it
+  if (s->trapz != SSD_TRAPZ_OFF && s->trapz != SSD_TRAPZ_DROP_BETA_DA && s->trapz != SSD_TRAPZ_EXACT_DA)
+    return SSD_ERR_INVALID;
+  if (s->trapz && (s->a_mode != SSD_A_PER_TOKEN || s->has_dt || s->has_init || s->has_dfinal || s->want_final ||
+                   s->want_A_cumsum || s->dA_skip))
+    return SSD_ERR_INVALID;
   if (s->chunk > SSD_MAX_CHUNK || s->headdim > SSD_MAX_HEADDIM || s->dstate > SSD_MAX_DSTATE)
     return SSD_ERR_UNSUPPORTED;
   if (s->varlen && s->nseq > kMaxSeq) return SSD_ERR_UNSUPPORTED;
@@ -72,6 +79,8 @@ int plan(const ssd_desc_t* s, Plan* p) {
   d.has_init = s->has_init != 0; d.has_dfinal = s->has_dfinal != 0; d.varlen = s->varlen != 0;
   d.eps = s->norm_eps;
   d.dA_skip = s->dA_skip;
+  d.trapz = s->trapz;
+  if (d.trapz) d.has_dt = 1;  // the scan's dt is gamma + rho (k_trapz_coef)
   p->dtype = s->dtype;
   p->state_dtype = s->state_dtype;
   p->fused_bwd = bwd_main_supported(p->dtype, d) ? 1 : 0;
@@ -111,6 +120,13 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_hin = take(MC * H * PN * es);
   p->o_ypre = d.has_z ? take((size_t)R * H * d.P * es) : 0;
   p->o_rstd = d.has_z ? take((size_t)R * sizeof(float)) : 0;
+  const size_t rh = (size_t)R * H * sizeof(float);
+  p->o_tzdt = d.trapz ? take(rh) : 0;
+  p->o_tzrho = d.trapz ? take(rh) : 0;
+  p->o_tzgam = d.trapz ? take(rh) : 0;
+  p->o_Dtok = d.trapz ? take(rh) : 0;
+  p->o_tzcb = d.trapz ? take((size_t)R * d.G * sizeof(float)) : 0;
+  p->o_hgam = d.trapz == SSD_TRAPZ_DROP_BETA_DA ? take(MC * H * PN * es) : 0;
   p->saved_bytes = off;
   off = 0;
   p->o_st = take(MC * H * PN * sizeof(float));
@@ -136,6 +152,9 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_dSf = tiles ? take(MC * d.G * nbq * nbq * 4096 * sizeof(float)) : 0;
   p->o_dst16 = tiles ? take(MC * H * PN * 2) : 0;
   p->o_dw = d.has_z ? take((size_t)p->norm_blocks * d.H * d.P * sizeof(float)) : 0;
+  p->o_xdy = d.trapz ? take(MC * H * d.Qpad * sizeof(float)) : 0;
+  p->o_tzddt = d.trapz ? take(rh) : 0;
+  p->o_tzda = d.trapz ? take(rh) : 0;
   p->bwd_bytes = off;
   return SSD_OK;
 }
@@ -156,6 +175,14 @@ void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
   b->fused_bwd = p.fused_bwd;
   b->nrowg = p.nrowg;
   b->ndcs = p.fused_bwd ? 2 : 1;
+  if (p.d.trapz) {
+    b->tz_dt = reinterpret_cast<float*>(s + p.o_tzdt);
+    b->tz_rho = reinterpret_cast<float*>(s + p.o_tzrho);
+    b->tz_gam = reinterpret_cast<float*>(s + p.o_tzgam);
+    b->Dtok = reinterpret_cast<float*>(s + p.o_Dtok);
+    b->tz_cb = reinterpret_cast<float*>(s + p.o_tzcb);
+    b->hgam = p.d.trapz == SSD_TRAPZ_DROP_BETA_DA ? s + p.o_hgam : nullptr;
+  }
 }
 
 void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
@@ -178,6 +205,11 @@ void bind_bwd(const Plan& p, void* scratch, SsdBufs* b) {
   b->dS_fix = tiles ? reinterpret_cast<float*>(s + p.o_dSf) : nullptr;
   b->dst16 = tiles ? reinterpret_cast<bf16*>(s + p.o_dst16) : nullptr;
   b->dw_part = p.d.has_z ? reinterpret_cast<float*>(s + p.o_dw) : nullptr;
+  if (p.d.trapz) {
+    b->xdy = reinterpret_cast<float*>(s + p.o_xdy);
+    b->tz_ddt = reinterpret_cast<float*>(s + p.o_tzddt);
+    b->tz_da = reinterpret_cast<float*>(s + p.o_tzda);
+  }
 }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -225,9 +257,9 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
   if (st != SSD_OK) return st;
   SsdDims& d = p.d;
   if (!a || !a->x || !a->A || !a->B || !a->C || !a->y) return SSD_ERR_INVALID;
-  if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight)) ||
+  if ((d.has_dt && !d.trapz && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight)) ||
       (d.has_init && !a->init) || (d.varlen && !a->cu_seqlens) || (desc->want_final && !a->final_state) ||
-      (desc->want_A_cumsum && !a->A_cumsum_out))
+      (desc->want_A_cumsum && !a->A_cumsum_out) || (d.trapz && (!a->gamma || !a->beta)))
     return SSD_ERR_INVALID;
   if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.fwd_bytes) return SSD_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -236,17 +268,36 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
   memset(&b, 0, sizeof(b));
   bind_saved(p, saved, &b);
   b.st = reinterpret_cast<float*>(scratch);
-  SsdIn in = {a->x, a->dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
+  // trapezoidal mode: the scan's dt is gamma + rho, written by the coefficient kernel
+  const float* dt = d.trapz ? b.tz_dt : a->dt;
+  SsdIn in = {a->x, dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
   const PhaseTimer tm{a->events, s};
+  const bool fused_state = state_fused_supported(p.dtype, d);
   SSD_PHASE(tm, SSD_PH_CHUNK_TABLE, launch_chunk_table(d, b, a->cu_seqlens, s));
   SSD_PHASE(tm, SSD_PH_CUMSUM,
-            launch_chunk_cumsum(p.dtype, d, b, a->A, a->dt, desc->want_A_cumsum ? a->A_cumsum_out : nullptr, s));
-  if (state_fused_supported(p.dtype, d)) {
+            launch_chunk_cumsum(p.dtype, d, b, a->A, dt, desc->want_A_cumsum ? a->A_cumsum_out : nullptr, s));
+  if (d.trapz) {
+    SSD_TRY(tm.begin(SSD_PH_TRAPZ_PREP));
+    SSD_TRY(launch_trapz_prep(p.dtype, d, b, a->A, a->gamma, a->beta, a->B, a->C, a->D, a->cu_seqlens, s));
+    if (d.trapz == SSD_TRAPZ_DROP_BETA_DA) {
+      // the gamma path's own states, for the backward's gamma-path decay gradient
+      SsdBufs bg = b;
+      bg.hin = b.hgam;
+      if (fused_state) {
+        SSD_TRY(launch_state_fwd_fused(d, bg, a->x, a->B, b.tz_gam, nullptr, nullptr, p.state_dtype, s));
+      } else {
+        SSD_TRY(launch_chunk_state(p.dtype, 0, d, bg, a->x, a->B, b.tz_gam, b.st, s));
+        SSD_TRY(launch_state_pass_fwd(p.dtype, p.state_dtype, d, bg, nullptr, nullptr, s));
+      }
+    }
+    SSD_TRY(tm.end(SSD_PH_TRAPZ_PREP));
+  }
+  if (fused_state) {
     SSD_PHASE(tm, SSD_PH_FWD_PASS,
-              launch_state_fwd_fused(d, b, a->x, a->B, a->dt, d.has_init ? a->init : nullptr,
+              launch_state_fwd_fused(d, b, a->x, a->B, dt, d.has_init ? a->init : nullptr,
                                      desc->want_final ? a->final_state : nullptr, p.state_dtype, s));
   } else {
-    SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, a->dt, b.st, s));
+    SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, dt, b.st, s));
     SSD_PHASE(tm, SSD_PH_FWD_PASS,
               launch_state_pass_fwd(p.dtype, p.state_dtype, d, b, d.has_init ? a->init : nullptr,
                                     desc->want_final ? a->final_state : nullptr, s));
@@ -334,7 +385,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   if (st != SSD_OK) return st;
   SsdDims& d = p.d;
   if (!a || !a->x || !a->A || !a->B || !a->C || !a->dy || !a->dx || !a->dB || !a->dC) return SSD_ERR_INVALID;
-  if ((d.has_dt && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight || !a->dz)) ||
+  if ((d.has_dt && !d.trapz && !a->dt) || (d.has_D && !a->D) || (d.has_z && (!a->z || !a->norm_weight || !a->dz)) ||
       (d.varlen && !a->cu_seqlens) || (d.has_dfinal && !a->dfinal))
     return SSD_ERR_INVALID;
   if (!saved || saved_bytes < p.saved_bytes || !scratch || scratch_bytes < p.bwd_bytes) return SSD_ERR_WORKSPACE;
@@ -344,7 +395,8 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   memset(&b, 0, sizeof(b));
   bind_saved(p, const_cast<void*>(saved), &b);
   bind_bwd(p, scratch, &b);
-  SsdIn in = {a->x, a->dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
+  const float* dt = d.trapz ? b.tz_dt : a->dt;
+  SsdIn in = {a->x, dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
   const PhaseTimer tm{a->events, s};
   // the fused backward needs 16-byte vector access; otherwise the column / row kernels run
   const bool fused = p.fused_bwd && d.vec_x && d.vec_bc;
@@ -353,6 +405,8 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
     b.nrowg = 1;           // column / row kernels write one rowG partial
     b.dst16 = nullptr;     // and read dst in fp32
   }
+  const bool fused_state = fused && state_fused_supported(p.dtype, d);
+  if (fused_state) b.npass_blk = state_fused_slices(d);  // dtot partials: one per headdim slice
   const void* dY = a->dy;
   if (d.has_z) {
     SSD_PHASE(tm, SSD_PH_NORM_BWD, launch_gated_norm_bwd(p.dtype, d, b, in, a->dy, a->dz, s));
@@ -360,42 +414,79 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
       SSD_PHASE(tm, SSD_PH_NORM_DW, launch_reduce_rows((int)p.norm_blocks, d.H * d.P, b.dw_part, a->dnorm_weight, s));
     dY = b.dyp;
   }
-  if (fused && state_fused_supported(p.dtype, d)) {
-    b.npass_blk = state_fused_slices(d);  // dtot partials: one per headdim slice
-    SSD_PHASE(tm, SSD_PH_BWD_PASS,
-              launch_state_bwd_fused(d, b, dY, a->C, d.has_dfinal ? a->dfinal : nullptr,
-                                     d.has_init ? a->dinit : nullptr, p.state_dtype, s));
-  } else {
-    SSD_PHASE(tm, SSD_PH_BWD_STATE, launch_chunk_state(p.dtype, 1, d, b, dY, a->C, a->dt, b.dst, s));
-    SSD_PHASE(tm, SSD_PH_BWD_PASS,
-              launch_state_pass_bwd(p.dtype, p.state_dtype, d, b, d.has_dfinal ? a->dfinal : nullptr,
-                                    d.has_init ? a->dinit : nullptr, s));
+  // One backward of the scan for (dd, bb, ii): the state pass (unless skipped: dst is then the one a
+  // previous pass left in the scratch), the column / row phases and the finish.
+  auto scan_bwd = [&](const SsdDims& dd, const SsdBufs& bb, const SsdIn& ii, const PhaseTimer& t, bool state_pass,
+                      float* ddt, void* dA_tok, float* da32) -> int {
+    if (state_pass) {
+      if (fused_state) {
+        SSD_PHASE(t, SSD_PH_BWD_PASS,
+                  launch_state_bwd_fused(dd, bb, dY, a->C, dd.has_dfinal ? a->dfinal : nullptr,
+                                         dd.has_init ? a->dinit : nullptr, p.state_dtype, s));
+      } else {
+        SSD_PHASE(t, SSD_PH_BWD_STATE, launch_chunk_state(p.dtype, 1, dd, bb, dY, a->C, ii.dt, bb.dst, s));
+        SSD_PHASE(t, SSD_PH_BWD_PASS,
+                  launch_state_pass_bwd(p.dtype, p.state_dtype, dd, bb, dd.has_dfinal ? a->dfinal : nullptr,
+                                        dd.has_init ? a->dinit : nullptr, s));
+      }
+    }
+    if (fused) {
+      // factorised column kernel, then the exact one on the (chunk, head) pairs it cannot take;
+      // the row phase builds dB / dC
+      SSD_TRY(t.begin(SSD_PH_BWD_COL));
+      SSD_TRY(launch_bwd_fact(dd, bb, ii, dY, a->dx, s));
+      SSD_TRY(launch_bwd_main(dd, bb, ii, dY, a->dx, true, s));
+      SSD_TRY(t.end(SSD_PH_BWD_COL));
+      SSD_PHASE(t, SSD_PH_BWD_ROW, launch_bwd_gemm(dd, bb, ii, dY, a->dB, a->dC, s));
+    } else {
+      SSD_PHASE(t, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, dd, bb, ii, dY, a->dx, a->dB, s));
+      SSD_PHASE(t, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, dd, bb, ii, dY, a->dC, s));
+    }
+    SSD_PHASE(t, SSD_PH_BWD_FINISH, launch_bwd_finish(p.dtype, dd, bb, ii, ddt, dA_tok, da32, s));
+    if (p.nslices > 1 && !fused) {
+      const int64_t nelem = dd.R * dd.G * dd.N;
+      SSD_TRY(t.begin(SSD_PH_BWD_REDUCE_BC));
+      SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, bb.dB_part, a->dB, s));
+      SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, bb.dC_part, a->dC, s));
+      SSD_TRY(t.end(SSD_PH_BWD_REDUCE_BC));
+    }
+    return SSD_OK;
+  };
+  if (d.trapz == SSD_TRAPZ_DROP_BETA_DA) {
+    // The reference's dA: the gamma path's alone, SSD(gamma x, a, B, C) over its own states, by a
+    // backward that computes the decay gradient only (the fused kernels skip dx, dS, dB, dC; the exact
+    // fixup and the column / row kernels still write dx / dB / dC, which the pass below overwrites).
+    SsdDims dg = d;
+    dg.trapz = SSD_TRAPZ_OFF;
+    dg.has_D = 0;
+    dg.has_z = 0;
+    dg.da_only = 1;
+    SsdBufs bg = b;
+    bg.hin = b.hgam;
+    bg.Dtok = nullptr;
+    SsdIn ig = in;
+    ig.dt = b.tz_gam;
+    const PhaseTimer none{nullptr, s};
+    SSD_TRY(tm.begin(SSD_PH_TRAPZ_GAMMA));
+    st = scan_bwd(dg, bg, ig, none, true, nullptr, nullptr, b.tz_da);
+    if (st != SSD_OK) return st;
+    SSD_TRY(tm.end(SSD_PH_TRAPZ_GAMMA));
   }
-  if (fused) {
-    // fused path: the column phase is the per-chunk kernel, the row phase builds dB / dC
-    // factorised column kernel, then the exact one on the (chunk, head) pairs it cannot take
-    SSD_TRY(tm.begin(SSD_PH_BWD_COL));
-    SSD_TRY(launch_bwd_fact(d, b, in, dY, a->dx, s));
-    SSD_TRY(launch_bwd_main(d, b, in, dY, a->dx, true, s));
-    SSD_TRY(tm.end(SSD_PH_BWD_COL));
-    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_gemm(d, b, in, dY, a->dB, a->dC, s));
-  } else {
-    SSD_PHASE(tm, SSD_PH_BWD_COL, launch_bwd_col(p.dtype, d, b, in, dY, a->dx, a->dB, s));
-    SSD_PHASE(tm, SSD_PH_BWD_ROW, launch_bwd_row(p.dtype, d, b, in, dY, a->dC, s));
-  }
-  SSD_PHASE(tm, SSD_PH_BWD_FINISH,
-            launch_bwd_finish(p.dtype, d, b, in, d.has_dt ? a->ddt : nullptr,
-                              (d.a_mode == SSD_A_PER_TOKEN ||
-                               (d.a_mode == SSD_A_CUMSUM && !(d.dA_skip & SSD_DA_SKIP_INTRA)))
-                                  ? a->dA
-                                  : nullptr,
-                              s));
-  if (p.nslices > 1 && !fused) {
-    const int64_t nelem = d.R * d.G * d.N;
-    SSD_TRY(tm.begin(SSD_PH_BWD_REDUCE_BC));
-    SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dB_part, a->dB, s));
-    SSD_TRY(launch_reduce_slices(p.dtype, nelem, (int)p.nslices, b.dC_part, a->dC, s));
-    SSD_TRY(tm.end(SSD_PH_BWD_REDUCE_BC));
+  // the scan of both paths (dt = gamma + rho, D per token); its dst equals the gamma pass's, which
+  // differs only in the decay term it feeds (h_in of the gamma path)
+  st = scan_bwd(d, b, in, tm, d.trapz != SSD_TRAPZ_DROP_BETA_DA, d.trapz ? b.tz_ddt : (d.has_dt ? a->ddt : nullptr),
+                d.trapz ? nullptr
+                        : ((d.a_mode == SSD_A_PER_TOKEN ||
+                            (d.a_mode == SSD_A_CUMSUM && !(d.dA_skip & SSD_DA_SKIP_INTRA)))
+                               ? a->dA
+                               : nullptr),
+                d.trapz == SSD_TRAPZ_EXACT_DA ? b.tz_da : nullptr);
+  if (st != SSD_OK) return st;
+  if (d.trapz) {
+    SSD_TRY(tm.begin(SSD_PH_TRAPZ_POST));
+    if (!fused) SSD_TRY(launch_trapz_bc(p.dtype, d, b, a->x, dY, a->B, a->C, a->dB, a->dC, a->cu_seqlens, s));
+    SSD_TRY(launch_trapz_grads(p.dtype, d, b, a->A, a->cu_seqlens, a->dgamma, a->dbeta, a->dA, s));
+    SSD_TRY(tm.end(SSD_PH_TRAPZ_POST));
   }
   float* dA_head = d.a_mode == SSD_A_PER_HEAD ? reinterpret_cast<float*>(a->dA) : nullptr;
   float* dD = d.has_D ? a->dD : nullptr;
@@ -438,6 +529,6 @@ const char* ssd_status_string(int status) {
   }
 }
 
-int ssd_abi_version(void) { return 3; }
+int ssd_abi_version(void) { return 4; }
 
 }  // extern "C"

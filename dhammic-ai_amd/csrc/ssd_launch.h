@@ -72,8 +72,9 @@ hipError_t launch_bwd_col(int dtype, const SsdDims& d, const SsdBufs& b, const S
                           const void* dy, void* dx, void* dB, hipStream_t s);
 hipError_t launch_bwd_row(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
                           const void* dy, void* dC, hipStream_t s);
+// ddt and da32 (fp32 per-token decay gradient, a_mode PER_TOKEN) are optional
 hipError_t launch_bwd_finish(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
-                             float* ddt, void* dA_tok, hipStream_t s);
+                             float* ddt, void* dA_tok, float* da32, hipStream_t s);
 size_t lds_bwd_col(int dtype, const SsdDims& d);
 size_t lds_bwd_row(int dtype, const SsdDims& d);
 
@@ -100,6 +101,16 @@ hipError_t launch_gated_norm_fwd(int dtype, const SsdDims& d, const SsdBufs& b, 
                                  void* y, hipStream_t s);
 hipError_t launch_gated_norm_bwd(int dtype, const SsdDims& d, const SsdBufs& b, const SsdIn& in,
                                  const void* dout, void* dz, hipStream_t s);
+
+// ssd_trapz.hip (trapezoidal mode): rho, dt = gamma + rho, C.B and D per token into b.tz_* / b.Dtok;
+// the column / row path's d(C.B) terms of dB and dC (and b.xdy); dgamma, dbeta, dA per token
+hipError_t launch_trapz_prep(int dtype, const SsdDims& d, const SsdBufs& b, const void* A, const void* gamma,
+                             const void* beta, const void* B, const void* C, const float* D, const int32_t* cu,
+                             hipStream_t s);
+hipError_t launch_trapz_bc(int dtype, const SsdDims& d, const SsdBufs& b, const void* x, const void* dy,
+                           const void* B, const void* C, void* dB, void* dC, const int32_t* cu, hipStream_t s);
+hipError_t launch_trapz_grads(int dtype, const SsdDims& d, const SsdBufs& b, const void* A, const int32_t* cu,
+                              void* dgamma, void* dbeta, void* dA, hipStream_t s);
 
 // ssd_reduce.hip
 hipError_t launch_reduce_slices(int dtype, int64_t nelem, int nslices, const float* part, void* out,

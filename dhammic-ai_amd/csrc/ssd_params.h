@@ -15,6 +15,8 @@ struct SsdDims {
   int a_mode, has_dt, has_D, has_z, has_init, has_dfinal, varlen;
   float eps;
   int dA_skip;                       // enum ssd_dA_skip bits (terms left out of the decay gradient)
+  int trapz;                         // enum ssd_trapz: dt is gamma + rho, D per token, strictly causal
+  int da_only;                       // backward for the decay gradient only (no dx / dB / dC / dS written)
   // 16-byte global loads allowed for x/dy/z-shaped tensors and for B/C (set per call
   // from the feature widths and the pointers' alignment)
   bool vec_x, vec_bc;
@@ -48,6 +50,19 @@ struct SsdBufs {
   float* dS_tiles;         // fused path: [nslices][max_chunks][G][nb*nb][64][64] head-summed dS
   float* dS_fix;           // fused path: [max_chunks][G][nb*nb][64][64] dS of the heads the exact fixup runs
   float* dw_part;          // [norm_blocks][H*P]
+  // trapezoidal mode (saved): rho = beta[t+1] exp(-a[t+1]); dt = gamma + rho; cb = C_t . B_t;
+  // Dtok = D + gamma cb (D per token; the scan is then strictly causal); gam = gamma in fp32;
+  // hgam = the gamma path's states (DROP_BETA_DA)
+  float* tz_dt;            // [R][H]
+  float* tz_rho;           // [R][H]
+  float* tz_gam;           // [R][H]
+  float* tz_cb;            // [R][G]
+  float* Dtok;             // [R][H] (nullptr outside trapezoidal mode)
+  void* hgam;              // [max_chunks][H][Ppad][Npad] (T)
+  // trapezoidal mode (backward scratch)
+  float* xdy;              // [max_chunks][H][Qpad] x_t . dy_t per head (the layout of xdx)
+  float* tz_ddt;           // [R][H] gradient at dt = gamma + rho
+  float* tz_da;            // [R][H] decay gradient of the scan (fp32)
   int npass_blk, nslices, hslice, norm_blocks;
   int fused_bwd;           // 1: k_bwd_main + k_bwd_gemm (bf16), 0: column / row kernels
   int ndcs;                // dcs_off partials

@@ -34,7 +34,7 @@ template <int PT, int NT>
 struct FwdLds {
   static constexpr int PP = 32 * PT, NP = 32 * NT;
   static size_t bytes(int nb) {
-    return 2 * (size_t)(nb * tsize<64, NP>() + nb * tsize<64, PP>() + tsize<PP, NP>()) + sizeof(float) * 2 * 64 * nb;
+    return 2 * (size_t)(nb * tsize<64, NP>() + nb * tsize<64, PP>() + tsize<PP, NP>()) + sizeof(float) * 3 * 64 * nb;
   }
 };
 
@@ -42,7 +42,7 @@ template <int PT, int NT, int NB>
 struct FwdStage {
   TileStage<64, 32 * PT, 256> x[NB];
   TileStage<32 * PT, 32 * NT, 256> hin;
-  float cs, dt;
+  float cs, dt, dtk;
 };
 
 }  // namespace
@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict__ chunks, const float* __restrict__ cs,
                  const bf16* __restrict__ hin, const bf16* __restrict__ x, const float* __restrict__ dt,
                  const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const float* __restrict__ Dv,
-                 bf16* __restrict__ y, const int32_t* __restrict__ fast) {
+                 bf16* __restrict__ y, const int32_t* __restrict__ fast, const float* __restrict__ Dtok) {
   constexpr int PP = 32 * PT, NP = 32 * NT;
   constexpr int XT = tsize<64, PP>(), CT = tsize<64, NP>();
   extern __shared__ __align__(16) unsigned char smem[];
@@ -80,6 +80,7 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
   bf16* ht = xt + NB * XT;                   // [PP][NP]
   float* s_cs2 = reinterpret_cast<float*>(ht + tsize<PP, NP>());  // [64 NB]
   float* s_dt = s_cs2 + 64 * NB;
+  float* s_dtk = s_dt + 64 * NB;  // trapezoidal mode: D per token
 
   // quadrants of this wave: slot 0 = (NB - 1 - w/2, 1 - w%2), slot 1 = (w/2, w%2)
   // while w/2 < NB - 2 (beyond that slot 0 of another wave already holds it);
@@ -142,9 +143,11 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
     tstage_load_v(st.hin, hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
     st.cs = 0.0f;
     st.dt = 1.0f;
+    st.dtk = 0.0f;
     if (threadIdx.x < 64 * NB) {
       st.cs = cs[((int64_t)c * d.H + h) * d.Qpad + threadIdx.x];
       if (d.has_dt && (int)threadIdx.x < ci.len) st.dt = dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
+      if (d.trapz && (int)threadIdx.x < ci.len) st.dtk = Dtok[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
     }
   };
   load_head(h_lo);
@@ -163,6 +166,7 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
     if (threadIdx.x < 64 * NB) {
       s_cs2[threadIdx.x] = st.cs * SSD_LOG2E;
       s_dt[threadIdx.x] = st.dt;
+      s_dtk[threadIdx.x] = st.dtk;
     }
     __syncthreads();
     if (h + 1 < h_hi) load_head(h + 1);
@@ -204,7 +208,7 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
         for (int v = 0; v < 16; ++v) {
           const float dd = cs_l - css[v];
           float mv = (float)S[u][v >> 3][v & 7] * exp2_fast(clamp_med3(dd, -SSD_T2, SSD_T2)) * dts[v];
-          if (diag && acc_row(v, lane) > (lane & 31)) mv = 0.0f;
+          if (diag && acc_row(v, lane) + (d.trapz ? 1 : 0) > (lane & 31)) mv = 0.0f;  // trapz: strict
           m[v] = mv;
         }
         const bf16* xj = xt + j * XT;
@@ -218,6 +222,7 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
       // epilogue: + D x, store y[l][p] (lane l writes 4 consecutive p per register group)
       if (lg < ci.len) {
         const bf16* xi = xt + i * XT;
+        const float Dl = d.trapz ? s_dtk[lg] : Dh;
         bf16* yrow = y + (int64_t)(ci.row0 + lg) * xrow + (int64_t)h * d.P;
 #pragma unroll
         for (int pt = 0; pt < PT; ++pt)
@@ -228,7 +233,7 @@ k_scan_fwd_chunk(SsdDims d, int hslice, int nslices, const ChunkInfo* __restrict
             const bf16x4 xv = tld4<PP>(xi, l_loc, p0);
             bf16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (bf16)(acc[pt][4 * r + e] + Dh * (float)xv[e]);
+            for (int e = 0; e < 4; ++e) o[e] = (bf16)(acc[pt][4 * r + e] + Dl * (float)xv[e]);
             *reinterpret_cast<bf16x4*>(yrow + p0) = o;
           }
       }
@@ -269,7 +274,7 @@ static hipError_t scan_fwd_chunk_t(const SsdDims& d, const SsdBufs& b, const Ssd
   hipLaunchKernelGGL((k_scan_fwd_chunk<PT, NT, NB>), dim3(d.max_chunks * d.G * ns), dim3(256), lds, s, d, hslice, ns,
                      b.chunks, b.cs, reinterpret_cast<const bf16*>(b.hin), reinterpret_cast<const bf16*>(in.x), in.dt,
                      reinterpret_cast<const bf16*>(in.B), reinterpret_cast<const bf16*>(in.C), in.D,
-                     reinterpret_cast<bf16*>(y), fast);
+                     reinterpret_cast<bf16*>(y), fast, b.Dtok);
   return hipGetLastError();
 }
 

@@ -105,13 +105,16 @@ struct FactCtx {
   const bf16* Bm;
   const bf16* Cm;
   const float* Dv;
+  const float* Dtok;   // trapezoidal mode: D per token, [R][H]
   bf16* y;
 };
 
 // The per-wave body: everything from the S units on, with the wave's quadrants,
 // units and p tile (pt) known at compile time. Block-wide barriers are reached
 // by every wave the same number of times.
-template <int PT, int NT, int NB, int Wq, int pt>
+// TZ: trapezoidal mode (strictly causal S, D per token), a compile-time switch so that the plain
+// kernel carries none of its code
+template <int PT, int NT, int NB, int Wq, int pt, bool TZ>
 __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned char* smem, int c, const ChunkInfo& ci,
                                           int g, int h_lo, int h_hi) {
   constexpr int PP = 32 * PT, NP = 32 * NT, NTHR = 256 * PT;
@@ -182,9 +185,10 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
              tld8<NP>(Ct + qi * CT, 32 * qlh + (lane & 31), n0));
       }
       if (uu == (q == 0 ? QD::n0 : QD::n1) - 1) {  // diagonal unit: s > l is outside the causal mask
+        constexpr int sd = TZ ? 1 : 0;              // (s >= l in trapezoidal mode)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          if (acc_row(v, lane) > (lane & 31)) sacc[v] = 0.0f;
+          if (acc_row(v, lane) + sd > (lane & 31)) sacc[v] = 0.0f;
       }
       S[u][0] = acc_frag(sacc, 0);
       S[u][1] = acc_frag(sacc, 1);
@@ -230,6 +234,18 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
     tstage_store<PP, NP, NTHR>(st.hin, ht);
     if (threadIdx.x < 64 * NB) s_cs2[threadIdx.x] = st.cs * SSD_LOG2E;
     __syncthreads();
+    // trapezoidal mode: D of this head at the lane's output row of each quadrant, loaded before the
+    // next head's prefetch so that waiting for it does not wait for the prefetch (the kernel's LDS
+    // is full at a 256-token chunk)
+    float dtk[2] = {0.0f, 0.0f};
+    if constexpr (TZ) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int i = q == 0 ? QD::i0 : QD::i1, lh = q == 0 ? QD::lh0 : QD::lh1;
+        const int lg = 64 * i + 32 * lh + (lane & 31);
+        if (i >= 0 && lg < ci.len) dtk[q] = a.Dtok[(int64_t)(ci.row0 + lg) * d.H + h];
+      }
+    }
     if (h + 1 < h_hi) load_head(h + 1);
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
 
@@ -270,7 +286,8 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
         mfma(acc, tld8<NP>(ht, 32 * pt + (lane & 31), kk + 8 * (lane >> 5)),
              tld8<NP>(Ct + i * CT, l_loc, kk + 8 * (lane >> 5)));
       // epilogue: * e_off, + D x (x from the output rows), into the output rows (lane l
-      // rewrites 4 consecutive p per register group)
+      // rewrites 4 consecutive p per register group); trapezoidal mode: D per token
+      const float Dl = TZ ? dtk[q] : Dh;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int p0 = 32 * pt + 8 * r + 4 * (lane >> 5);
@@ -278,7 +295,7 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
         const bf16x4 xv = *op;
         bf16x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (bf16)fmaf(acc[4 * r + e], e_off, Dh * (float)xv[e]);
+        for (int e = 0; e < 4; ++e) o[e] = (bf16)fmaf(acc[4 * r + e], e_off, Dl * (float)xv[e]);
         *op = o;
       }
     }
@@ -288,7 +305,7 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
   store_out(h_hi - 1);
 }
 
-template <int PT, int NT, int NB>
+template <int PT, int NT, int NB, bool TZ>
 __global__ void __launch_bounds__(256 * PT) __attribute__((amdgpu_waves_per_eu(PT, PT)))
 k_scan_fwd_fact(FactCtx<PT, NT, NB> a) {
   constexpr int NP = 32 * NT, NTHR = 256 * PT;
@@ -316,14 +333,14 @@ k_scan_fwd_fact(FactCtx<PT, NT, NB> a) {
   }
   __syncthreads();
   switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
-    case 0: fact_body<PT, NT, NB, 0, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 1: fact_body<PT, NT, NB, 1, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 2: fact_body<PT, NT, NB, 2, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 3: fact_body<PT, NT, NB, 3, 0>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 4: fact_body<PT, NT, NB, 0, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 5: fact_body<PT, NT, NB, 1, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
-    case 6: fact_body<PT, NT, NB, 2, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
-    default: fact_body<PT, NT, NB, 3, PT - 1>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 0: fact_body<PT, NT, NB, 0, 0, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 1: fact_body<PT, NT, NB, 1, 0, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 2: fact_body<PT, NT, NB, 2, 0, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 3: fact_body<PT, NT, NB, 3, 0, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 4: fact_body<PT, NT, NB, 0, PT - 1, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 5: fact_body<PT, NT, NB, 1, PT - 1, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    case 6: fact_body<PT, NT, NB, 2, PT - 1, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
+    default: fact_body<PT, NT, NB, 3, PT - 1, TZ>(a, smem, c, ci, g, h_lo, h_hi); break;
   }
 }
 
@@ -362,9 +379,16 @@ static hipError_t scan_fwd_fact_t(const SsdDims& d, const SsdBufs& b, const SsdI
   a.Bm = reinterpret_cast<const bf16*>(in.B);
   a.Cm = reinterpret_cast<const bf16*>(in.C);
   a.Dv = in.D;
+  a.Dtok = b.Dtok;
   a.y = reinterpret_cast<bf16*>(y);
-  ensure_lds(k_scan_fwd_fact<PT, NT, NB>, lds);
-  hipLaunchKernelGGL((k_scan_fwd_fact<PT, NT, NB>), dim3(d.max_chunks * d.G * ns), dim3(256 * PT), lds, s, a);
+  if (d.trapz) {
+    ensure_lds(k_scan_fwd_fact<PT, NT, NB, true>, lds);
+    hipLaunchKernelGGL((k_scan_fwd_fact<PT, NT, NB, true>), dim3(d.max_chunks * d.G * ns), dim3(256 * PT), lds, s, a);
+  } else {
+    ensure_lds(k_scan_fwd_fact<PT, NT, NB, false>, lds);
+    hipLaunchKernelGGL((k_scan_fwd_fact<PT, NT, NB, false>), dim3(d.max_chunks * d.G * ns), dim3(256 * PT), lds, s,
+                       a);
+  }
   return hipGetLastError();
 }
 

@@ -26,7 +26,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                                                         const float* __restrict__ cs, const T* __restrict__ hin,
                                                         const T* __restrict__ x, const float* __restrict__ dt,
                                                         const T* __restrict__ Bm, const T* __restrict__ Cm,
-                                                        const float* __restrict__ Dv, T* __restrict__ y) {
+                                                        const float* __restrict__ Dv, T* __restrict__ y,
+                                                        const float* __restrict__ Dtok) {
   constexpr int PPAD = 32 * PT, NPAD = 32 * NT;
   constexpr int NP = lds_pitch<T>(NPAD), BP = lds_pitch<T>(SSD_BLK);
   constexpr int MYT = (PT + 1) / 2;  // p tiles per wave
@@ -109,7 +110,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int v = 0; v < 16; ++v) {
           const int s = sb + acc_row(v, lane);
           const float m = st[v] * exp_clamp(cs_l[k] - css[v]) * dts[v];
-          X[v] = (s <= l_me && l_ok) ? m : 0.0f;
+          X[v] = (s + (d.trapz ? 1 : 0) <= l_me && l_ok) ? m : 0.0f;  // trapezoidal mode: strictly causal
         }
         const AccFrags<T> xf = acc_frags<T>(X);
 #pragma unroll
@@ -136,7 +137,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (l >= ci.len) continue;
         const int64_t o = (int64_t)(ci.row0 + l) * xrow + (int64_t)h * d.P + p;
         float yv = acc[k][tt][v];
-        if (d.has_D) yv += Dh * to_f(x[o]);
+        // trapezoidal mode: D per token
+        if (d.has_D || d.trapz) yv += (d.trapz ? Dtok[(int64_t)(ci.row0 + l) * d.H + h] : Dh) * to_f(x[o]);
         y[o] = from_f<T>(yv);
       }
     }
@@ -166,7 +168,7 @@ hipError_t scan_fwd_t(const SsdDims& d, const SsdBufs& b, const SsdIn& in, void*
   hipLaunchKernelGGL((k_chunk_scan_fwd<T, HS, PT, NT>), grid, dim3(256), lds, s, d, b.chunks, b.cs,
                      reinterpret_cast<const T*>(b.hin), reinterpret_cast<const T*>(in.x), in.dt,
                      reinterpret_cast<const T*>(in.B), reinterpret_cast<const T*>(in.C), in.D,
-                     reinterpret_cast<T*>(y));
+                     reinterpret_cast<T*>(y), b.Dtok);
   return hipGetLastError();
 }
 

@@ -1,0 +1,198 @@
+// Trapezoidal two-SSD mode: the coefficient kernels around the one scan that
+// computes both SSD calls of r2/dhammic-ai/src/mamba_base_engine.py:167-183,
+//   y = SSD(gamma x, a, B, C) + SSD(beta x_prev, a, B_prev, C),
+// x_prev[t] = x[t-1], B_prev[t] = B[t-1], both zero at a sequence's first token.
+//
+// With rho[t] = beta[t+1] exp(-a[t+1]) (zero at a sequence's last token), the
+// state h~[t] = exp(a[t]) h~[t-1] + (gamma[t] + rho[t]) x[t] B[t]^T equals the
+// sum of the two paths' states plus rho[t] x[t] B[t]^T, the beta input of token
+// t+1 taken in one step early (exp(a[t+1]) rho[t] = beta[t+1]). So
+//   y[t] = C[t] h~[t] - rho[t] (C[t] . B[t]) x[t]
+//        = sum_{s < t} (C[t] . B[s]) L[t, s] (gamma + rho)[s] x[s] + state term + gamma[t] (C[t] . B[t]) x[t]:
+// the scan runs once, strictly causal, with dt = gamma + rho, and the diagonal
+// term is a per-token D, D[t] = D + gamma (C . B). The gradient at dt of the
+// strict scan is drho, dgamma = drho + (C . B)(x . dy), dbeta[t+1] =
+// drho[t] exp(-a[t+1]) and, through both paths (EXACT_DA), da[t+1] -= drho[t]
+// rho[t]; d(C . B) = sum_h gamma (x . dy) enters dB and dC as the diagonal of
+// dS. Nothing is subtracted, so no gradient loses digits to cancellation.
+//
+// The reference's second call reuses the first call's cache (L, decay_chunk,
+// A_cumsum), so the beta path contributes nothing to dA (ssd_scan.py:476-533);
+// DROP_BETA_DA keeps that: its dA is the gamma path's alone, from a second
+// backward of SSD(gamma x, a, B, C) over the gamma path's states.
+#include "ssd_launch.h"
+#include "ssd_tile.h"
+
+namespace {
+
+// [start, end) of the sequence holding `row` and its index (end = start: row is in none)
+__device__ __forceinline__ int tz_seq(const SsdDims& d, const int32_t* __restrict__ cu, int64_t row, int64_t& start,
+                                      int64_t& end) {
+  if (!d.varlen) {
+    const int s = (int)(row / d.seqlen);
+    start = (int64_t)s * d.seqlen;
+    end = start + d.seqlen;
+    return s;
+  }
+  const int64_t R = d.R;
+  int lo = 0, hi = d.nseq - 1;  // last s with cu[s] <= row (offsets clamped as the chunk table does)
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (min<int64_t>(max(cu[mid], 0), R) <= row) lo = mid; else hi = mid - 1;
+  }
+  start = min<int64_t>(max(cu[lo], 0), R);
+  end = min<int64_t>(max<int64_t>(cu[lo + 1], start), R);
+  if (row < start || row >= end) end = start = row;
+  return lo;
+}
+
+// Index of `row` (in sequence `seq` starting at `start`) in the [max_chunks][H][Qpad] per-position
+// arrays, head 0: chunks restart at every sequence start (k_chunk_table).
+__device__ __forceinline__ int64_t tz_pos(const SsdDims& d, const SsdBufs& b, int64_t row, int64_t start, int seq) {
+  const int64_t c0 = d.varlen ? b.seq_chunk0[seq] : (int64_t)seq * ((d.seqlen + d.Q - 1) / d.Q);
+  const int64_t k = (row - start) / d.Q;
+  return (c0 + k) * d.H * d.Qpad + (row - start - k * d.Q);
+}
+
+}  // namespace
+
+// cb[row][g] = C[row, g] . B[row, g]; one wave per (row, group), lanes over the state dim.
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapz_cb(SsdDims d, const T* __restrict__ B, const T* __restrict__ C,
+                                                  float* __restrict__ cb) {
+  const int64_t row = blockIdx.x;
+  const int g = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (g >= d.G) return;
+  const int64_t o = (row * d.G + g) * d.N;
+  float s = 0.0f;
+  for (int n = lane; n < d.N; n += 64) s += to_f(B[o + n]) * to_f(C[o + n]);
+  for (int m = 32; m > 0; m >>= 1) s += __shfl_xor(s, m, 64);
+  if (lane == 0) cb[row * d.G + g] = s;
+}
+
+// Per (row, head): rho, dt = gamma + rho, gamma in fp32, D per token = D + gamma cb.
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapz_coef(SsdDims d, const int32_t* __restrict__ cu,
+                                                    const T* __restrict__ A, const T* __restrict__ gamma,
+                                                    const T* __restrict__ beta, const float* __restrict__ D,
+                                                    SsdBufs b) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= d.R * d.H) return;
+  const int64_t row = id / d.H;
+  const int h = (int)(id - row * d.H);
+  int64_t start, end;
+  tz_seq(d, cu, row, start, end);
+  float rho = 0.0f;
+  if (row + 1 < end) rho = to_f(beta[id + d.H]) * exp2_fast(-to_f(A[id + d.H]) * SSD_LOG2E);
+  const float gm = to_f(gamma[id]);
+  b.tz_rho[id] = rho;
+  b.tz_gam[id] = gm;
+  b.tz_dt[id] = gm + rho;
+  b.Dtok[id] = (d.has_D ? D[h] : 0.0f) + gm * b.tz_cb[row * d.G + h / d.hpg];
+}
+
+// Column / row path only (the fused path does this inside k_bwd_fact and k_bwd_gemm): per (row, group)
+// xdy = x . dy per head, and d(C . B) = sum_h gamma xdy into dB (+= . C) and dC (+= . B).
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapz_bc(SsdDims d, const int32_t* __restrict__ cu,
+                                                  const T* __restrict__ x, const T* __restrict__ dy,
+                                                  const T* __restrict__ B, const T* __restrict__ C,
+                                                  T* __restrict__ dB, T* __restrict__ dC, SsdBufs b) {
+  const int64_t row = blockIdx.x;
+  const int g = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (g >= d.G) return;
+  int64_t start, end;
+  const int seq = tz_seq(d, cu, row, start, end);
+  if (row >= end) return;  // in no sequence
+  const int64_t pos = tz_pos(d, b, row, start, seq);
+  float dcb = 0.0f;
+  for (int h = g * d.hpg; h < (g + 1) * d.hpg; ++h) {
+    const int64_t o = (row * d.H + h) * d.P;
+    float s = 0.0f;
+    for (int p = lane; p < d.P; p += 64) s += to_f(x[o + p]) * to_f(dy[o + p]);
+    for (int m = 32; m > 0; m >>= 1) s += __shfl_xor(s, m, 64);
+    if (lane == 0) b.xdy[pos + (int64_t)h * d.Qpad] = s;
+    dcb += b.tz_gam[row * d.H + h] * s;
+  }
+  const int64_t o = (row * d.G + g) * d.N;
+  for (int n = lane; n < d.N; n += 64) {
+    dB[o + n] = from_f<T>(to_f(dB[o + n]) + dcb * to_f(C[o + n]));
+    dC[o + n] = from_f<T>(to_f(dC[o + n]) + dcb * to_f(B[o + n]));
+  }
+}
+
+// Per (row, head), after the finish kernel: drho = d(dt) of the strict scan, dgamma = drho + cb xdy;
+// drho of the previous token gives dbeta = drho exp(-a) and (EXACT_DA) the decay term -drho rho;
+// dA = the scan's decay gradient + that.
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapz_grads(SsdDims d, const int32_t* __restrict__ cu,
+                                                     const T* __restrict__ A, SsdBufs b, T* __restrict__ dgamma,
+                                                     T* __restrict__ dbeta, T* __restrict__ dA) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= d.R * d.H) return;
+  const int64_t row = id / d.H;
+  const int h = (int)(id - row * d.H);
+  int64_t start, end;
+  const int seq = tz_seq(d, cu, row, start, end);
+  const bool inside = row < end;
+  if (dgamma)
+    dgamma[id] = from_f<T>(inside ? b.tz_ddt[id] + b.tz_cb[row * d.G + h / d.hpg] *
+                                                       b.xdy[tz_pos(d, b, row, start, seq) + (int64_t)h * d.Qpad]
+                                  : 0.0f);
+  float drho = 0.0f, rho = 0.0f;
+  if (row > start && inside) {
+    drho = b.tz_ddt[id - d.H];
+    rho = b.tz_rho[id - d.H];
+  }
+  if (dbeta) dbeta[id] = from_f<T>(drho * exp2_fast(-to_f(A[id]) * SSD_LOG2E));
+  if (dA) dA[id] = from_f<T>(inside ? b.tz_da[id] - (d.trapz == 2 ? drho * rho : 0.0f) : 0.0f);
+}
+
+template <typename T>
+static hipError_t trapz_prep_t(const SsdDims& d, const SsdBufs& b, const void* A, const void* gamma, const void* beta,
+                               const void* B, const void* C, const float* D, const int32_t* cu, hipStream_t s) {
+  hipLaunchKernelGGL(k_trapz_cb<T>, dim3((unsigned)d.R, (d.G + 3) / 4), dim3(256), 0, s, d,
+                     reinterpret_cast<const T*>(B), reinterpret_cast<const T*>(C), b.tz_cb);
+  const int64_t n = d.R * d.H;
+  hipLaunchKernelGGL(k_trapz_coef<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d, cu,
+                     reinterpret_cast<const T*>(A), reinterpret_cast<const T*>(gamma),
+                     reinterpret_cast<const T*>(beta), D, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_trapz_prep(int dtype, const SsdDims& d, const SsdBufs& b, const void* A, const void* gamma,
+                             const void* beta, const void* B, const void* C, const float* D, const int32_t* cu,
+                             hipStream_t s) {
+  return dtype == 1 ? trapz_prep_t<bf16>(d, b, A, gamma, beta, B, C, D, cu, s)
+                    : trapz_prep_t<float>(d, b, A, gamma, beta, B, C, D, cu, s);
+}
+
+hipError_t launch_trapz_bc(int dtype, const SsdDims& d, const SsdBufs& b, const void* x, const void* dy,
+                           const void* B, const void* C, void* dB, void* dC, const int32_t* cu, hipStream_t s) {
+  const dim3 grid((unsigned)d.R, (d.G + 3) / 4);
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_trapz_bc<bf16>, grid, dim3(256), 0, s, d, cu, reinterpret_cast<const bf16*>(x),
+                       reinterpret_cast<const bf16*>(dy), reinterpret_cast<const bf16*>(B),
+                       reinterpret_cast<const bf16*>(C), reinterpret_cast<bf16*>(dB), reinterpret_cast<bf16*>(dC), b);
+  else
+    hipLaunchKernelGGL(k_trapz_bc<float>, grid, dim3(256), 0, s, d, cu, reinterpret_cast<const float*>(x),
+                       reinterpret_cast<const float*>(dy), reinterpret_cast<const float*>(B),
+                       reinterpret_cast<const float*>(C), reinterpret_cast<float*>(dB), reinterpret_cast<float*>(dC),
+                       b);
+  return hipGetLastError();
+}
+
+hipError_t launch_trapz_grads(int dtype, const SsdDims& d, const SsdBufs& b, const void* A, const int32_t* cu,
+                              void* dgamma, void* dbeta, void* dA, hipStream_t s) {
+  const int64_t n = d.R * d.H;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == 1)
+    hipLaunchKernelGGL(k_trapz_grads<bf16>, grid, dim3(256), 0, s, d, cu, reinterpret_cast<const bf16*>(A), b,
+                       reinterpret_cast<bf16*>(dgamma), reinterpret_cast<bf16*>(dbeta), reinterpret_cast<bf16*>(dA));
+  else
+    hipLaunchKernelGGL(k_trapz_grads<float>, grid, dim3(256), 0, s, d, cu, reinterpret_cast<const float*>(A), b,
+                       reinterpret_cast<float*>(dgamma), reinterpret_cast<float*>(dbeta), reinterpret_cast<float*>(dA));
+  return hipGetLastError();
+}

@@ -36,16 +36,22 @@ SSD_DA_SKIP_INTRA = 1
 SSD_DA_SKIP_CUMSUM = 2
 SSD_DA_SKIP_CHUNK = 4
 
+# enum ssd_trapz
+SSD_TRAPZ_OFF = 0
+SSD_TRAPZ_DROP_BETA_DA = 1
+SSD_TRAPZ_EXACT_DA = 2
+
 # enum ssd_phase (launch order of ssd_fwd / ssd_bwd)
 PHASES = ("chunk_table", "cumsum", "fwd_state", "fwd_pass", "fwd_scan", "norm_fwd", "norm_bwd", "norm_dw",
-          "bwd_state", "bwd_pass", "bwd_col", "bwd_row", "bwd_finish", "bwd_reduce_bc", "bwd_reduce_heads")
+          "bwd_state", "bwd_pass", "bwd_col", "bwd_row", "bwd_finish", "bwd_reduce_bc", "bwd_reduce_heads",
+          "trapz_prep", "trapz_gamma", "trapz_post")
 SSD_NUM_PHASES = len(PHASES)
 
 SSD_WS_SAVED = 0
 SSD_WS_FWD_SCRATCH = 1
 SSD_WS_BWD_SCRATCH = 2
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -59,7 +65,7 @@ class SsdDesc(ctypes.Structure):
         ("dtype", _i32), ("state_dtype", _i32), ("a_mode", _i32),
         ("has_dt", _i32), ("has_D", _i32), ("has_z", _i32), ("has_init", _i32),
         ("has_dfinal", _i32), ("varlen", _i32), ("want_final", _i32), ("want_A_cumsum", _i32),
-        ("norm_eps", ctypes.c_float), ("dA_skip", _i32),
+        ("norm_eps", ctypes.c_float), ("dA_skip", _i32), ("trapz", _i32),
     ]
 
 
@@ -68,7 +74,8 @@ _IN_FIELDS = [("x", _vp), ("dt", _vp), ("A", _vp), ("B", _vp), ("C", _vp), ("D",
 
 
 class SsdFwdArgs(ctypes.Structure):
-    _fields_ = _IN_FIELDS + [("y", _vp), ("final_state", _vp), ("A_cumsum_out", _vp), ("events", _vp)]
+    _fields_ = _IN_FIELDS + [("y", _vp), ("final_state", _vp), ("A_cumsum_out", _vp), ("events", _vp),
+                             ("gamma", _vp), ("beta", _vp)]
 
 
 class SsdBwdArgs(ctypes.Structure):
@@ -76,6 +83,7 @@ class SsdBwdArgs(ctypes.Structure):
         ("dy", _vp), ("dfinal", _vp),
         ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp), ("dC", _vp), ("dD", _vp),
         ("dz", _vp), ("dnorm_weight", _vp), ("dinit", _vp), ("events", _vp),
+        ("gamma", _vp), ("beta", _vp), ("dgamma", _vp), ("dbeta", _vp),
     ]
 
 

@@ -63,6 +63,7 @@ class _Cfg:
     want_acs: bool
     eps: float
     dA_skip: int = 0
+    trapz: int = 0   # enum ssd_trapz (fused_trapezoidal_ssd_scan)
 
 
 def _desc(cfg: _Cfg, x, B, dt, D, z, init, has_dfinal=False):
@@ -79,10 +80,11 @@ def _desc(cfg: _Cfg, x, B, dt, D, z, init, has_dfinal=False):
     d.has_init = int(init is not None)
     d.has_dfinal = int(has_dfinal)
     d.varlen = int(cfg.varlen)
-    d.want_final = 1
+    d.want_final = int(not cfg.trapz)
     d.want_A_cumsum = int(cfg.want_acs)
     d.norm_eps = cfg.eps
     d.dA_skip = cfg.dA_skip
+    d.trapz = cfg.trapz
     return d
 
 
@@ -92,11 +94,12 @@ def _check_device(*ts):
             raise AssertionError("fused SSD scan: all tensors must be on the GPU (got a CPU tensor)")
 
 
-def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None):
-    """Run ssd_fwd. Returns (y, final_state, A_cumsum_out or empty, saved workspace).
-    ``events``: optional ctypes array of 2*SSD_NUM_PHASES hipEvent_t (profiling)."""
+def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None, gamma=None, beta=None):
+    """Run ssd_fwd. Returns (y, final_state or None, A_cumsum_out or empty, saved workspace).
+    ``events``: optional ctypes array of 2*SSD_NUM_PHASES hipEvent_t (profiling); ``gamma``,
+    ``beta``: the trapezoidal mode's coefficients (cfg.trapz)."""
     lib = C_.load()
-    _check_device(x, dt, A, B, C, D, z, w, init, cu)
+    _check_device(x, dt, A, B, C, D, z, w, init, cu, gamma, beta)
     desc = _desc(cfg, x, B, dt, D, z, init)
     C_.check(lib.ssd_validate(ctypes.byref(desc)), "ssd_fwd")
     b, T, H, P = x.shape
@@ -104,7 +107,7 @@ def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None):
     dev = x.device
     y = torch.empty_like(x)
     sdt = torch.float32 if cfg.state_code == C_.SSD_DTYPE_F32 else torch.bfloat16
-    final = torch.empty((cfg.nseq, H, P, N), dtype=sdt, device=dev)
+    final = None if cfg.trapz else torch.empty((cfg.nseq, H, P, N), dtype=sdt, device=dev)
     acs = (torch.empty((b, H, T // cfg.chunk, cfg.chunk), dtype=x.dtype, device=dev)
            if cfg.want_acs else x.new_empty(0))
     saved = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_SAVED), dtype=torch.uint8,
@@ -113,7 +116,7 @@ def _forward(cfg: _Cfg, x, dt, A, B, C, D, z, w, init, cu, events=None):
                           dtype=torch.uint8, device=dev)
     args = C_.SsdFwdArgs(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(w), _p(init), _p(cu),
                          _p(y), _p(final), _p(acs) if cfg.want_acs else None,
-                         None if events is None else ctypes.cast(events, ctypes.c_void_p))
+                         None if events is None else ctypes.cast(events, ctypes.c_void_p), _p(gamma), _p(beta))
     with torch.cuda.device(dev):
         st = lib.ssd_fwd(ctypes.byref(desc), ctypes.byref(args), _p(saved), saved.numel(), _p(scratch),
                          scratch.numel(), _stream(dev))
@@ -132,7 +135,8 @@ def _dA_out(cfg: _Cfg, x, A):
     return None
 
 
-def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal, events=None):
+def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal, events=None, gamma=None,
+              beta=None):
     """Run ssd_bwd. Returns dict of gradients (None where the input is absent).
     ``A`` is the decay input the forward took (A_cumsum with a cache)."""
     lib = C_.load()
@@ -152,6 +156,8 @@ def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal
         "z": torch.empty_like(z) if z is not None else None,
         "w": torch.empty_like(w) if (w is not None and z is not None) else None,
         "init": torch.empty_like(init) if init is not None else None,
+        "gamma": torch.empty_like(gamma) if gamma is not None else None,
+        "beta": torch.empty_like(beta) if beta is not None else None,
     }
     scratch = torch.empty(lib.ssd_workspace_bytes(ctypes.byref(desc), C_.SSD_WS_BWD_SCRATCH),
                           dtype=torch.uint8, device=dev)
@@ -159,7 +165,8 @@ def _backward(cfg: _Cfg, saved_ws, x, dt, A, B, C, D, z, w, init, cu, dy, dfinal
                          _p(dy), _p(dfinal),
                          _p(g["x"]), _p(g["dt"]), _p(g["A"]), _p(g["B"]), _p(g["C"]), _p(g["D"]),
                          _p(g["z"]), _p(g["w"]), _p(g["init"]),
-                         None if events is None else ctypes.cast(events, ctypes.c_void_p))
+                         None if events is None else ctypes.cast(events, ctypes.c_void_p),
+                         _p(gamma), _p(beta), _p(g["gamma"]), _p(g["beta"]))
     with torch.cuda.device(dev):
         st = lib.ssd_bwd(ctypes.byref(desc), ctypes.byref(args), _p(saved_ws), saved_ws.numel(), _p(scratch),
                          scratch.numel(), _stream(dev))

@@ -1,0 +1,103 @@
+"""The trapezoidal block's two SSD calls as one scan on MI355X.
+
+``Mamba3Block._forward_impl`` (r2/dhammic-ai/src/mamba_base_engine.py:167-191) runs
+
+    y_gamma, _, cache = fused_ssd_scan(x * gamma, dA, B, C, chunk)
+    B_prev, x_prev    = B, x shifted one token later (zero at t = 0)
+    y_beta, _, _      = fused_ssd_scan(x_prev * beta, dA, B_prev, C, chunk, cache=cache)
+    y = (y_gamma + y_beta)[:, :T] + x * D;  y = rmsnorm(y) * silu(z)
+
+with (dt, dA, beta, gamma) from the trapezoidal coefficients (``trapezoidal.py:7-13``:
+gamma = lam dt, beta = (1 - lam) dt exp(dA)). ``fused_trapezoidal_ssd_scan`` computes the same
+y with one pass of the scan kernels: with rho[t] = beta[t+1] exp(-dA[t+1]) the pair is
+SSD((gamma + rho) x, dA, B, C) - rho (C.B) x exactly, so the decay, the C B^T tiles, the state
+passes and the gated norm are shared (the coefficient kernels are in csrc/ssd_trapz.hip; the scan
+runs strictly causal with the diagonal folded into a per-token D + gamma (C.B)). The rewrite's
+rounding is that of one SSD call as long as rho is of the order of gamma, which the trapezoidal
+coefficients guarantee (beta exp(-dA) = (1 - lam) dt). Where a per-token decay is steeper than
+about -8 the reference's e^-20 clamp floor (ssd_scan.py:53-54) lands on a different exponent for
+the beta path, which moves dbeta by up to e^(-20 - dA) times its terms (the other outputs and
+gradients keep the clamp's e^-20 bound).
+
+Gradients: the reference's second call reuses the first call's cache, so the beta path's decay
+gives dA nothing (ssd_scan.py:476-533). ``exact_beta_dA=False`` (the default) returns that
+gradient; ``exact_beta_dA=True`` returns the gradient of y through both paths. dx, dgamma, dbeta,
+dB, dC, dD, dz and dnorm_weight are the full gradients in both settings (in the reference they
+flow through both calls alike).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _capi as C_
+from .ssd_scan import _Cfg, _backward, _check_device, _forward
+
+__all__ = ["fused_trapezoidal_ssd_scan"]
+
+
+class _TrapzFunction(torch.autograd.Function):
+    """Autograd node over ssd_fwd / ssd_bwd in trapezoidal mode (inputs contiguous)."""
+
+    @staticmethod
+    def forward(ctx, cfg, x, dA, gamma, beta, B, C, D, z, w, cu):
+        ctx.set_materialize_grads(False)
+        y, _, _, saved = _forward(cfg, x, None, dA, B, C, D, z, w, None, cu, gamma=gamma, beta=beta)
+        ctx.cfg = cfg
+        ctx.ws = saved
+        ctx.save_for_backward(x, dA, gamma, beta, B, C, D, z, w, cu)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        if dy is None:
+            return (None,) * 11
+        x, dA, gamma, beta, B, C, D, z, w, cu = ctx.saved_tensors
+        g = _backward(ctx.cfg, ctx.ws, x, None, dA, B, C, D, z, w, None, cu, dy, None, gamma=gamma, beta=beta)
+        ni = ctx.needs_input_grad
+        pick = lambda k, i: g[k] if ni[i] else None  # noqa: E731
+        return (None, pick("x", 1), pick("A", 2), pick("gamma", 3), pick("beta", 4), pick("B", 5), pick("C", 6),
+                pick("D", 7), pick("z", 8), pick("w", 9), None)
+
+
+def fused_trapezoidal_ssd_scan(x, dA, gamma, beta, B, C, chunk_size, D=None, z=None, norm_weight=None,
+                               norm_eps=1e-6, exact_beta_dA=False, cu_seqlens=None):
+    """y = SSD(x*gamma, dA, B, C) + SSD(x_prev*beta, dA, B_prev, C) [+ D*x] [then rmsnorm(y)*w*silu(z)].
+
+    x (b, T, H, P); dA, gamma, beta (b, T, H); B, C (b, T, G, N) with head h reading group
+    h // (H/G) (the reference block passes per-head B, C: G = H); all in one dtype, bf16 or fp32.
+    D (H,); z (b, T, H, P) or (b, T, H*P); norm_weight (H*P,) (ones when z is given without it).
+    T need not be a chunk multiple (the reference zero-pads, :154-165; here the last chunk is
+    partial). cu_seqlens (nseq+1,) int32 packs sequences along T (b must be 1); the shift then
+    restarts at every sequence start. Returns y (b, T, H, P) in x's dtype.
+    """
+    b, T, H, P = x.shape
+    _check_device(x, dA, gamma, beta, B, C, D, z, norm_weight)
+    dt_ = x.dtype
+    for name, t in (("dA", dA), ("gamma", gamma), ("beta", beta), ("B", B), ("C", C)):
+        if t.dtype != dt_:
+            raise RuntimeError(f"fused_trapezoidal_ssd_scan: {name} must have x's dtype {dt_} (got {t.dtype})")
+    for name, t in (("dA", dA), ("gamma", gamma), ("beta", beta)):
+        if tuple(t.shape) != (b, T, H):
+            raise ValueError(f"fused_trapezoidal_ssd_scan: {name} must be {(b, T, H)} (got {tuple(t.shape)})")
+    if B.shape[:2] != (b, T) or C.shape != B.shape:
+        raise ValueError("fused_trapezoidal_ssd_scan: B and C must be (b, T, G, N)")
+    f32 = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
+    cu = None
+    nseq = b
+    if cu_seqlens is not None:
+        if b != 1:
+            raise ValueError("fused_trapezoidal_ssd_scan: cu_seqlens needs batch == 1")
+        cu = cu_seqlens.to(device=x.device, dtype=torch.int32).contiguous()
+        nseq = cu.numel() - 1
+    if z is not None:
+        z = z.reshape(b, T, H, P).contiguous()
+        if z.dtype != dt_:
+            raise RuntimeError("fused_trapezoidal_ssd_scan: z must have x's dtype")
+        if norm_weight is None:
+            norm_weight = torch.ones(H * P, dtype=torch.float32, device=x.device)
+    mode = C_.SSD_TRAPZ_EXACT_DA if exact_beta_dA else C_.SSD_TRAPZ_DROP_BETA_DA
+    cfg = _Cfg(chunk=int(chunk_size), a_mode=C_.SSD_A_PER_TOKEN, nseq=nseq, varlen=cu is not None,
+               state_code=C_.SSD_DTYPE_F32, want_acs=False, eps=float(norm_eps), trapz=mode)
+    return _TrapzFunction.apply(cfg, x.contiguous(), dA.contiguous(), gamma.contiguous(), beta.contiguous(),
+                                B.contiguous(), C.contiguous(), f32(D), z,
+                                f32(norm_weight) if z is not None else None, cu)

@@ -83,6 +83,30 @@ enum ssd_dA_skip {
   SSD_DA_SKIP_CHUNK = 4
 };
 
+/* Trapezoidal two-SSD mode (ssd_desc_t.trapz), the caller's pair of SSD calls
+ * in r2/dhammic-ai/src/mamba_base_engine.py:167-191:
+ *   y = SSD(gamma*x, a, B, C) + SSD(beta*x_prev, a, B_prev, C)  [+ D*x] [gated norm]
+ * with x_prev[t] = x[t-1], B_prev[t] = B[t-1] (zero at each sequence's first
+ * token), a = A per token (a_mode PER_TOKEN) and gamma, beta (b, seqlen, h) in
+ * dtype (trapezoidal.py:7-13). Computed as ONE scan: with
+ * rho[t] = beta[t+1] exp(-a[t+1]) (0 at a sequence's last token) the pair equals
+ * SSD((gamma + rho)*x, a, B, C) - rho[t] (C[t].B[t]) x[t] exactly (the state then
+ * carries the beta input of the next token one step early); the kernels run that
+ * scan strictly causal with the diagonal as a per-token D, D + gamma[t] (C[t].B[t]).
+ * The rounding is that of one SSD call while rho is of the order of gamma, which
+ * the trapezoidal coefficients give (beta exp(-a) = (1 - lam) dt). The reference's
+ * second call reuses the first call's cache, so the beta path gives no decay
+ * gradient (ssd_scan.py:533): DROP_BETA_DA reproduces that, EXACT_DA returns
+ * the gradient of the pair through both paths. dA is then (b, seqlen, h) in
+ * dtype, and ssd_bwd_args_t.dgamma / dbeta receive the other two gradients.
+ * Requires a_mode PER_TOKEN, has_dt == 0, has_init == 0, want_A_cumsum == 0,
+ * dA_skip == 0; the ssd_*_args_t gamma and beta pointers. */
+enum ssd_trapz {
+  SSD_TRAPZ_OFF = 0,
+  SSD_TRAPZ_DROP_BETA_DA = 1,   /* the reference's gradients (beta path: no dA)  */
+  SSD_TRAPZ_EXACT_DA = 2        /* dA through both paths                         */
+};
+
 /* Kernel limits: chunk <= 256, headdim <= 128, dstate <= 128. */
 #define SSD_MAX_CHUNK 256
 #define SSD_MAX_HEADDIM 128
@@ -99,6 +123,7 @@ typedef struct ssd_desc {
   int32_t want_A_cumsum; /* ssd_fwd writes A_cumsum_out (needs varlen == 0)          */
   float norm_eps;        /* gated RMSNorm epsilon (has_z)                            */
   int32_t dA_skip;       /* enum ssd_dA_skip bits; 0: the full gradient              */
+  int32_t trapz;         /* enum ssd_trapz                                           */
 } ssd_desc_t;
 
 /* Kernel launches of ssd_fwd / ssd_bwd, in launch order. For profiling, a
@@ -112,7 +137,11 @@ enum ssd_phase {
   SSD_PH_NORM_BWD = 6, SSD_PH_NORM_DW = 7, SSD_PH_BWD_STATE = 8, SSD_PH_BWD_PASS = 9,
   SSD_PH_BWD_COL = 10, SSD_PH_BWD_ROW = 11, SSD_PH_BWD_FINISH = 12, SSD_PH_BWD_REDUCE_BC = 13,
   SSD_PH_BWD_REDUCE_HEADS = 14,
-  SSD_NUM_PHASES = 15
+  /* trapz: the coefficient kernel (and, DROP_BETA_DA, the gamma-path state pass)
+   * of the forward; the gamma-path backward (DROP_BETA_DA) and the per-token
+   * gradient kernels of the backward */
+  SSD_PH_TRAPZ_PREP = 15, SSD_PH_TRAPZ_GAMMA = 16, SSD_PH_TRAPZ_POST = 17,
+  SSD_NUM_PHASES = 18
 };
 
 typedef struct ssd_fwd_args {
@@ -121,6 +150,7 @@ typedef struct ssd_fwd_args {
   const int32_t* cu_seqlens;
   void* y; void* final_state; void* A_cumsum_out;
   void* const* events;   /* optional, see enum ssd_phase */
+  const void* gamma; const void* beta;   /* trapz: (batch, seqlen, nheads) dtype */
 } ssd_fwd_args_t;
 
 typedef struct ssd_bwd_args {
@@ -131,6 +161,8 @@ typedef struct ssd_bwd_args {
   void* dx; float* ddt; void* dA; void* dB; void* dC; float* dD; void* dz;
   float* dnorm_weight; void* dinit;
   void* const* events;   /* optional, see enum ssd_phase */
+  const void* gamma; const void* beta;   /* trapz: as in ssd_fwd_args_t           */
+  void* dgamma; void* dbeta;             /* trapz: (batch, seqlen, nheads) dtype  */
 } ssd_bwd_args_t;
 
 enum ssd_workspace_kind {

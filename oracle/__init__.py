@@ -21,5 +21,9 @@ Contents
                    RMSNorm, initial/final state, packed varlen) that the
                    extended entry point computes; defined by composition over
                    ``ssd_chunked`` (no counterpart in the reference).
+``trapezoidal``    the reference block's two SSD calls (gamma path, shifted beta path
+                   reusing the cache, + D x, gated norm; mamba_base_engine.py:
+                   152-191) over ``ssd_chunked``, and the same pair as two fp64
+                   token recurrences that pin it (tests/test_trapz_oracle.py).
 ``inputs``         seeded input generators with BASELINE's distributions.
 """

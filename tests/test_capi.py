@@ -89,6 +89,10 @@ def test_validation_accepts_benchmark_configs(capi):
     # reference API: per-token A, no dt, state in the input dtype
     assert _validate(capi, a_mode=capi.SSD_A_PER_TOKEN, has_dt=0, has_D=0, has_z=0, ngroups=64,
                      state_dtype=capi.SSD_DTYPE_BF16, want_A_cumsum=1) == capi.SSD_OK
+    # trapezoidal mode at config 4's layer shape (per-head B/C), both gradient settings
+    for mode in (capi.SSD_TRAPZ_DROP_BETA_DA, capi.SSD_TRAPZ_EXACT_DA):
+        assert _validate(capi, batch=4, seqlen=4096, nheads=32, ngroups=32, a_mode=capi.SSD_A_PER_TOKEN,
+                         has_dt=0, want_final=0, trapz=mode) == capi.SSD_OK
     # reference cache path: cached A_cumsum, with and without a cached L
     for skip in (6, 7):
         assert _validate(capi, a_mode=capi.SSD_A_CUMSUM, has_dt=0, has_D=0, has_z=0, ngroups=64,
@@ -108,6 +112,13 @@ def test_validation_accepts_benchmark_configs(capi):
     # a cached A_cumsum (cumsum mode) carries no gradient: CUMSUM and CHUNK must be skipped
     (dict(a_mode=2, has_dt=0, dA_skip=0), "SSD_ERR_INVALID"),
     (dict(a_mode=2, has_dt=0, dA_skip=2), "SSD_ERR_INVALID"),
+    # trapezoidal mode: per-token decay, no dt, no initial / final state, no cache options
+    (dict(trapz=3, a_mode=1, has_dt=0, want_final=0), "SSD_ERR_INVALID"),
+    (dict(trapz=1, has_dt=0, want_final=0), "SSD_ERR_INVALID"),              # per-head A
+    (dict(trapz=1, a_mode=1, has_dt=1, want_final=0), "SSD_ERR_INVALID"),    # dt given
+    (dict(trapz=2, a_mode=1, has_dt=0, want_final=1), "SSD_ERR_INVALID"),    # final state asked
+    (dict(trapz=2, a_mode=1, has_dt=0, want_final=0, has_init=1), "SSD_ERR_INVALID"),
+    (dict(trapz=1, a_mode=1, has_dt=0, want_final=0, dA_skip=7), "SSD_ERR_INVALID"),
     (dict(chunk=512), "SSD_ERR_UNSUPPORTED"),
     (dict(headdim=256), "SSD_ERR_UNSUPPORTED"),
     (dict(dstate=160), "SSD_ERR_UNSUPPORTED"),

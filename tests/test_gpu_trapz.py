@@ -1,0 +1,137 @@
+"""GPU parity of fused_trapezoidal_ssd_scan: the trapezoidal block's two SSD calls
+(r2/dhammic-ai/src/mamba_base_engine.py:167-191) computed as one scan, against the oracle's
+two-call composition (oracle/trapezoidal.py, itself pinned on the CPU by two fp64 token
+recurrences, tests/test_trapz_oracle.py).
+
+Inputs follow the reference's producers: gamma = lam dt, beta = (1 - lam) dt exp(dA)
+(trapezoidal.py:7-13). Both gradient settings: the reference's (the beta path's decay gives dA
+nothing, its second call reuses the cache) and the exact one. Every output and gradient (x, dA,
+gamma, beta, B, C, D, z, norm weight) is checked normwise (max|got - ref| / max|ref|) to 1e-4
+for fp32 inputs and 1e-2 for bf16 inputs (the oracle in fp32/fp64 on the same bf16 values).
+
+Cases cover the kernel paths: the factorised forward and backward (P <= 64), the exact fixup
+(steep decays: every 64-token block drops more than the factorised range), the column / row
+path (P = 128), groups shared by several heads, packed sequences with an empty one, lengths that
+are not chunk multiples, and config 4's layer shape (B=4, L=4096, H=32, P=64, per-head N=128).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from oracle.trapezoidal import two_call_ssd
+from ssd_testlib import TOL, rel_err
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs an MI355X (HIP device)")]
+
+DEV = "cuda"
+NAMES = ("x", "dA", "gamma", "beta", "B", "C", "D", "z", "w")
+
+
+@pytest.fixture(autouse=True)
+def _fp32_matmul():
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+    torch.backends.cuda.matmul.allow_tf32 = prev
+    torch.cuda.empty_cache()
+
+
+def make(b, T, H, P, G, N, dtype, seed=0, steep=False, with_z=True):
+    """The block's SSD inputs in `dtype` (CPU), and dy."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    if steep:  # a in about [-2.2, -1]: every 64-token block drops more than the factorised range (64 nats)
+        dt = torch.nn.functional.softplus(0.3 * r(b, T, H) + 1.2)
+        A = -torch.empty(H).uniform_(0.9, 1.2, generator=g)
+    else:
+        dt = torch.nn.functional.softplus(r(b, T, H) - 1.0)
+        A = -torch.exp(torch.empty(H).uniform_(-4.0, -1.0, generator=g))
+    lam = torch.sigmoid(r(b, T, H))
+    dA = dt * A
+    t = {"x": r(b, T, H, P), "dA": dA, "gamma": lam * dt, "beta": (1.0 - lam) * dt * torch.exp(dA),
+         "B": r(b, T, G, N), "C": r(b, T, G, N), "D": r(H), "dy": r(b, T, H, P)}
+    if with_z:
+        t["z"] = r(b, T, H, P)
+        t["w"] = 1.0 + 0.1 * r(H * P)
+    for k in ("x", "dA", "gamma", "beta", "B", "C", "dy", "z"):
+        if k in t:
+            t[k] = t[k].to(dtype)
+    return t
+
+
+def native(t, Q, exact, cu=None):
+    import kernels
+    leaves = {k: v.to(DEV).requires_grad_(True) for k, v in t.items() if k != "dy"}
+    y = kernels.fused_trapezoidal_ssd_scan(
+        leaves["x"], leaves["dA"], leaves["gamma"], leaves["beta"], leaves["B"], leaves["C"], Q, D=leaves["D"],
+        z=leaves.get("z"), norm_weight=leaves.get("w"), exact_beta_dA=exact,
+        cu_seqlens=None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV))
+    y.backward(t["dy"].to(DEV))
+    torch.cuda.synchronize()
+    return y.detach(), {k: v.grad for k, v in leaves.items()}
+
+
+def oracle(t, Q, exact, cu=None, device="cpu", dtype=torch.float64):
+    leaves = {k: v.to(device=device, dtype=dtype).requires_grad_(True) for k, v in t.items() if k != "dy"}
+    y = two_call_ssd(leaves["x"], leaves["dA"], leaves["gamma"], leaves["beta"], leaves["B"], leaves["C"], Q,
+                     D=leaves["D"], z=leaves.get("z"), norm_weight=leaves.get("w"), exact_beta_dA=exact,
+                     cu_seqlens=cu)
+    y.backward(t["dy"].to(device=device, dtype=dtype))
+    return y.detach(), {k: v.grad for k, v in leaves.items()}
+
+
+def check(t, Q, exact, dtype, cu=None, oracle_device="cpu", oracle_dtype=torch.float64, tag=""):
+    y, g = native(t, Q, exact, cu)
+    yr, gr = oracle(t, Q, exact, cu, oracle_device, oracle_dtype)
+    tol = TOL[dtype]
+    errs = {"y": rel_err(y, yr)}
+    for k in NAMES:
+        if k in g:
+            errs[k] = rel_err(g[k], gr[k])
+    print(f"  {tag} exact={exact}: " + " ".join(f"{k} {e:.1e}" for k, e in errs.items()), flush=True)
+    for k, e in errs.items():
+        assert e <= tol, f"{k}: rel err {e:.3e} > {tol:.0e}"
+    return errs
+
+
+MODES = [False, True]
+MODE_IDS = ["drop_beta_dA", "exact_dA"]
+
+
+@pytest.mark.parametrize("exact", MODES, ids=MODE_IDS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [
+    dict(b=2, T=200, H=4, P=32, G=4, N=32, Q=64),     # ragged length, per-head B/C
+    dict(b=1, T=256, H=4, P=64, G=2, N=64, Q=128),    # two heads per group
+    dict(b=2, T=160, H=2, P=128, G=2, N=64, Q=64),    # P = 128: column / row kernels
+], ids=["ragged", "groups", "p128"])
+def test_trapezoidal_small(shape, dtype, exact):
+    s = dict(shape)
+    Q = s.pop("Q")
+    check(make(**s, dtype=dtype, seed=1), Q, exact, dtype, tag=f"{s} {dtype}")
+
+
+@pytest.mark.parametrize("exact", MODES, ids=MODE_IDS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_trapezoidal_steep_decay_takes_the_exact_kernels(dtype, exact):
+    t = make(2, 192, 4, 64, 4, 64, dtype, seed=2, steep=True)
+    assert (t["dA"].float().mean() < -1.1), "steep inputs should leave the factorised range"
+    check(t, 64, exact, dtype, tag=f"steep {dtype}")
+
+
+@pytest.mark.parametrize("exact", MODES, ids=MODE_IDS)
+def test_trapezoidal_packed_sequences(exact):
+    cu = [0, 70, 70, 201, 300]
+    t = make(1, 300, 4, 32, 4, 32, torch.float32, seed=3)
+    check(t, 64, exact, torch.float32, cu=cu, tag="packed")
+
+
+@pytest.mark.parametrize("exact", MODES, ids=MODE_IDS)
+def test_trapezoidal_config4_layer(exact):
+    """Config 4's layer: B=4, L=4096, H=32, P=64, per-head B/C with N=128, chunk 256, bf16, with the
+    block's D and gated norm; the oracle runs in fp32 on the GPU on the same bf16 values."""
+    t = make(4, 4096, 32, 64, 32, 128, torch.bfloat16, seed=4)
+    check(t, 256, exact, torch.bfloat16, oracle_device=DEV, oracle_dtype=torch.float32, tag="config4 layer")
