@@ -1,0 +1,261 @@
+// Block front-end kernels (gfx950): the trapezoidal coefficients
+// (r2/dhammic-ai/src/kernels/trapezoidal.py:3-52) and the data-dependent rotary
+// embedding of B and C (rope.py:4-10), forward and backward, with the C ABI of
+// include/ssd_frontend.h. All of them are elementwise streams bound by HBM:
+// one thread per element (or per rotation pair), fp32 in registers, the storage
+// dtype at the edges. The head-parameter gradients of the trapezoidal backward
+// are per-block partial sums reduced in a fixed order (k_reduce_rows), so the
+// result does not depend on scheduling.
+#include "ssd_frontend.h"
+#include "ssd_launch.h"
+#include "ssd_mi355x.h"
+
+namespace {
+
+constexpr int kTzRows = 4;         // row lanes per block of the trapezoidal backward
+constexpr int kTzMaxBlocks = 1024; // row blocks (partials) of the trapezoidal backward
+
+int64_t tz_row_blocks(int64_t rows) {
+  const int64_t nb = (rows + kTzRows - 1) / kTzRows;
+  return nb < kTzMaxBlocks ? nb : kTzMaxBlocks;
+}
+
+template <typename T>
+__device__ __forceinline__ float ld0(const T* p, int64_t i) {
+  return p ? to_f(p[i]) : 0.0f;
+}
+
+__device__ __forceinline__ float softplus_f(float s) { return fmaxf(s, 0.0f) + log1pf(expf(-fabsf(s))); }
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+}  // namespace
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapezoidal_fwd(int64_t n, int H, const T* __restrict__ dt_raw,
+                                                         const T* __restrict__ lam_raw, const T* __restrict__ dt_bias,
+                                                         const T* __restrict__ A_log, T* __restrict__ dt,
+                                                         T* __restrict__ dA, T* __restrict__ beta,
+                                                         T* __restrict__ gamma) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int h = (int)(i % H);
+    const float d = softplus_f(to_f(dt_raw[i]) + to_f(dt_bias[h]));
+    const float lam = sigmoid_f(to_f(lam_raw[i]));
+    const float a = -expf(to_f(A_log[h]));
+    const float da = d * a;
+    dt[i] = from_f<T>(d);
+    dA[i] = from_f<T>(da);
+    beta[i] = from_f<T>((1.0f - lam) * d * expf(da));
+    gamma[i] = from_f<T>(lam * d);
+  }
+}
+
+// Backward: block (64 heads, kTzRows row lanes), grid (row blocks, head tiles). Per element
+// (trapezoidal.py:28-52):
+//   g_dt_total = g_dt + g_dA A + g_beta (1 - lam) alpha (1 + dA) + g_gamma lam
+//   g_lam      = -g_beta dt alpha + g_gamma dt
+//   g_A        = g_dA dt + g_beta (1 - lam) dt^2 alpha
+//   d_dt_raw = g_dt_total sigmoid(s),  d_lam_raw = g_lam lam (1 - lam),
+//   partials: d_dt_bias += d_dt_raw,   d_A_log += g_A A
+template <typename T>
+__global__ void __launch_bounds__(256) k_trapezoidal_bwd(int64_t rows, int H, const T* __restrict__ dt_raw,
+                                                         const T* __restrict__ lam_raw, const T* __restrict__ dt_bias,
+                                                         const T* __restrict__ A_log, const T* __restrict__ g_dt,
+                                                         const T* __restrict__ g_dA, const T* __restrict__ g_beta,
+                                                         const T* __restrict__ g_gamma, T* __restrict__ d_dt_raw,
+                                                         T* __restrict__ d_lam_raw, float* __restrict__ part_bias,
+                                                         float* __restrict__ part_alog) {
+  __shared__ float red[2][kTzRows][64];
+  const int hx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int h = blockIdx.y * 64 + hx;
+  float pb = 0.0f, pa = 0.0f;
+  if (h < H) {
+    const float bias = to_f(dt_bias[h]);
+    const float a = -expf(to_f(A_log[h]));
+    for (int64_t r = (int64_t)blockIdx.x * kTzRows + ty; r < rows; r += (int64_t)gridDim.x * kTzRows) {
+      const int64_t i = r * H + h;
+      const float s = to_f(dt_raw[i]) + bias;
+      const float d = softplus_f(s);
+      const float sig = sigmoid_f(s);
+      const float lam = sigmoid_f(to_f(lam_raw[i]));
+      const float da = d * a;
+      const float alpha = expf(da);
+      const float gd = ld0(g_dt, i), gA = ld0(g_dA, i), gb = ld0(g_beta, i), gg = ld0(g_gamma, i);
+      const float gtot = gd + gA * a + gb * (1.0f - lam) * alpha * (1.0f + da) + gg * lam;
+      const float glam = -gb * d * alpha + gg * d;
+      const float gAr = gA * d + gb * (1.0f - lam) * d * d * alpha;
+      const float ddr = gtot * sig;
+      d_dt_raw[i] = from_f<T>(ddr);
+      d_lam_raw[i] = from_f<T>(glam * lam * (1.0f - lam));
+      pb += ddr;
+      pa += gAr * a;
+    }
+  }
+  red[0][ty][hx] = pb;
+  red[1][ty][hx] = pa;
+  __syncthreads();
+  if (ty == 0 && h < H) {
+    float sb = 0.0f, sa = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kTzRows; ++k) {
+      sb += red[0][k][hx];
+      sa += red[1][k][hx];
+    }
+    part_bias[(int64_t)blockIdx.x * H + h] = sb;
+    part_alog[(int64_t)blockIdx.x * H + h] = sa;
+  }
+}
+
+// Rotary embedding. PER_HEAD: one thread per rotation pair (b, t, h, k); otherwise one thread per
+// (b, t, k) looping over the heads, so that the shared angle's gradient is summed in registers.
+template <typename T, typename TA, bool PER_HEAD>
+__global__ void __launch_bounds__(256) k_rope(int64_t n, int H, int half, const T* __restrict__ x,
+                                              const TA* __restrict__ ang, const T* __restrict__ dy,
+                                              T* __restrict__ out, TA* __restrict__ dang) {
+  const bool bwd = dy != nullptr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / half;  // (b, t, h) with PER_HEAD, else (b, t)
+    const int k = (int)(i - row * half);
+    float s, c;
+    sincosf(to_f(ang[i]), &s, &c);
+    const int hn = PER_HEAD ? 1 : H;
+    float gacc = 0.0f;
+    for (int hh = 0; hh < hn; ++hh) {
+      const int64_t o = ((PER_HEAD ? row : row * H + hh) * half + k) * 2;
+      const float x1 = to_f(x[o]), x2 = to_f(x[o + 1]);
+      if (!bwd) {
+        out[o] = from_f<T>(c * x1 - s * x2);
+        out[o + 1] = from_f<T>(s * x1 + c * x2);
+      } else {
+        const float g1 = to_f(dy[o]), g2 = to_f(dy[o + 1]);
+        out[o] = from_f<T>(c * g1 + s * g2);       // the inverse rotation
+        out[o + 1] = from_f<T>(-s * g1 + c * g2);
+        gacc += g1 * (-s * x1 - c * x2) + g2 * (c * x1 - s * x2);
+      }
+    }
+    if (bwd) dang[i] = from_f<TA>(gacc);
+  }
+}
+
+namespace {
+
+unsigned grid_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
+}
+
+template <typename T>
+int trapz_fwd_t(int64_t rows, int64_t H, const void* a, const void* b, const void* c, const void* d, void* o1,
+                void* o2, void* o3, void* o4, hipStream_t s) {
+  const int64_t n = rows * H;
+  hipLaunchKernelGGL(k_trapezoidal_fwd<T>, dim3(grid_for(n)), dim3(256), 0, s, n, (int)H,
+                     static_cast<const T*>(a), static_cast<const T*>(b), static_cast<const T*>(c),
+                     static_cast<const T*>(d), static_cast<T*>(o1), static_cast<T*>(o2), static_cast<T*>(o3),
+                     static_cast<T*>(o4));
+  return hipGetLastError() == hipSuccess ? SSD_OK : SSD_ERR_HIP;
+}
+
+template <typename T>
+int trapz_bwd_t(int64_t rows, int64_t H, const void* dtr, const void* lr, const void* bias, const void* alog,
+                const void* gd, const void* gA, const void* gb, const void* gg, void* ddr, void* dlr, float* dbias,
+                float* dalog, void* ws, hipStream_t s) {
+  const int64_t nb = tz_row_blocks(rows);
+  float* pb = static_cast<float*>(ws);
+  float* pa = pb + nb * H;
+  hipLaunchKernelGGL(k_trapezoidal_bwd<T>, dim3((unsigned)nb, (unsigned)((H + 63) / 64)), dim3(64 * kTzRows), 0, s,
+                     rows, (int)H, static_cast<const T*>(dtr), static_cast<const T*>(lr), static_cast<const T*>(bias),
+                     static_cast<const T*>(alog), static_cast<const T*>(gd), static_cast<const T*>(gA),
+                     static_cast<const T*>(gb), static_cast<const T*>(gg), static_cast<T*>(ddr), static_cast<T*>(dlr),
+                     pb, pa);
+  if (hipGetLastError() != hipSuccess) return SSD_ERR_HIP;
+  if (launch_reduce_rows((int)nb, (int)H, pb, dbias, s) != hipSuccess) return SSD_ERR_HIP;
+  if (launch_reduce_rows((int)nb, (int)H, pa, dalog, s) != hipSuccess) return SSD_ERR_HIP;
+  return SSD_OK;
+}
+
+template <typename T, typename TA>
+int rope_t(int64_t B, int64_t L, int64_t H, int64_t half, int per_head, const void* x, const void* ang,
+           const void* dy, void* out, void* dang, hipStream_t s) {
+  const int64_t n = B * L * (per_head ? H : 1) * half;
+  auto* xp = static_cast<const T*>(x);
+  auto* ap = static_cast<const TA*>(ang);
+  auto* gp = static_cast<const T*>(dy);
+  auto* op = static_cast<T*>(out);
+  auto* dp = static_cast<TA*>(dang);
+  if (per_head)
+    hipLaunchKernelGGL((k_rope<T, TA, true>), dim3(grid_for(n)), dim3(256), 0, s, n, (int)H, (int)half, xp, ap, gp,
+                       op, dp);
+  else
+    hipLaunchKernelGGL((k_rope<T, TA, false>), dim3(grid_for(n)), dim3(256), 0, s, n, (int)H, (int)half, xp, ap, gp,
+                       op, dp);
+  return hipGetLastError() == hipSuccess ? SSD_OK : SSD_ERR_HIP;
+}
+
+bool dtype_ok(int32_t t) { return t == SSD_DTYPE_F32 || t == SSD_DTYPE_BF16; }
+
+int rope_dispatch(int32_t dtype, int32_t adtype, int64_t B, int64_t L, int64_t H, int64_t half, int32_t per_head,
+                  const void* x, const void* ang, const void* dy, void* out, void* dang, void* stream) {
+  if (!dtype_ok(dtype) || !dtype_ok(adtype) || B < 1 || L < 1 || H < 1 || half < 1 || !x || !ang || !out)
+    return SSD_ERR_INVALID;
+  if (dy && !dang) return SSD_ERR_INVALID;
+  if (B * L * H * half > INT64_MAX / 4 || H > INT32_MAX || half > INT32_MAX) return SSD_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SSD_DTYPE_BF16)
+    return adtype == SSD_DTYPE_BF16 ? rope_t<bf16, bf16>(B, L, H, half, per_head, x, ang, dy, out, dang, s)
+                                    : rope_t<bf16, float>(B, L, H, half, per_head, x, ang, dy, out, dang, s);
+  return adtype == SSD_DTYPE_BF16 ? rope_t<float, bf16>(B, L, H, half, per_head, x, ang, dy, out, dang, s)
+                                  : rope_t<float, float>(B, L, H, half, per_head, x, ang, dy, out, dang, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssd_trapezoidal_fwd(int32_t dtype, int64_t rows, int64_t nheads, const void* dt_raw, const void* lam_raw,
+                        const void* dt_bias, const void* A_log, void* dt, void* dA, void* beta, void* gamma,
+                        void* stream) {
+  if (!dtype_ok(dtype) || rows < 1 || nheads < 1 || !dt_raw || !lam_raw || !dt_bias || !A_log || !dt || !dA ||
+      !beta || !gamma)
+    return SSD_ERR_INVALID;
+  if (nheads > INT32_MAX || rows > INT64_MAX / nheads) return SSD_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == SSD_DTYPE_BF16 ? trapz_fwd_t<bf16>(rows, nheads, dt_raw, lam_raw, dt_bias, A_log, dt, dA, beta, gamma, s)
+                                 : trapz_fwd_t<float>(rows, nheads, dt_raw, lam_raw, dt_bias, A_log, dt, dA, beta, gamma, s);
+}
+
+size_t ssd_trapezoidal_bwd_workspace(int64_t rows, int64_t nheads) {
+  if (rows < 1 || nheads < 1) return 0;
+  return (size_t)(2 * tz_row_blocks(rows) * nheads) * sizeof(float);
+}
+
+int ssd_trapezoidal_bwd(int32_t dtype, int64_t rows, int64_t nheads, const void* dt_raw, const void* lam_raw,
+                        const void* dt_bias, const void* A_log, const void* g_dt, const void* g_dA,
+                        const void* g_beta, const void* g_gamma, void* d_dt_raw, void* d_lam_raw, float* d_dt_bias,
+                        float* d_A_log, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype) || rows < 1 || nheads < 1 || !dt_raw || !lam_raw || !dt_bias || !A_log || !d_dt_raw ||
+      !d_lam_raw || !d_dt_bias || !d_A_log)
+    return SSD_ERR_INVALID;
+  if (nheads > INT32_MAX || rows > INT64_MAX / nheads) return SSD_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < ssd_trapezoidal_bwd_workspace(rows, nheads)) return SSD_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == SSD_DTYPE_BF16
+             ? trapz_bwd_t<bf16>(rows, nheads, dt_raw, lam_raw, dt_bias, A_log, g_dt, g_dA, g_beta, g_gamma, d_dt_raw,
+                                 d_lam_raw, d_dt_bias, d_A_log, workspace, s)
+             : trapz_bwd_t<float>(rows, nheads, dt_raw, lam_raw, dt_bias, A_log, g_dt, g_dA, g_beta, g_gamma,
+                                  d_dt_raw, d_lam_raw, d_dt_bias, d_A_log, workspace, s);
+}
+
+int ssd_rope_fwd(int32_t dtype, int32_t angle_dtype, int64_t batch, int64_t seqlen, int64_t nheads,
+                 int64_t half_dim, int32_t per_head, const void* x, const void* angles, void* out, void* stream) {
+  return rope_dispatch(dtype, angle_dtype, batch, seqlen, nheads, half_dim, per_head, x, angles, nullptr, out,
+                       nullptr, stream);
+}
+
+int ssd_rope_bwd(int32_t dtype, int32_t angle_dtype, int64_t batch, int64_t seqlen, int64_t nheads,
+                 int64_t half_dim, int32_t per_head, const void* x, const void* angles, const void* dy, void* dx,
+                 void* dangles, void* stream) {
+  if (!dy) return SSD_ERR_INVALID;
+  return rope_dispatch(dtype, angle_dtype, batch, seqlen, nheads, half_dim, per_head, x, angles, dy, dx, dangles,
+                       stream);
+}
+
+}  // extern "C"

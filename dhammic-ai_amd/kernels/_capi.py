@@ -87,9 +87,11 @@ class SsdBwdArgs(ctypes.Structure):
     ]
 
 
-# Every symbol include/ssd_mi355x.h declares.
+# Every symbol include/ssd_mi355x.h and include/ssd_frontend.h declare.
 EXPORTS = ("ssd_validate", "ssd_workspace_bytes", "ssd_fwd", "ssd_fwd_noalloc", "ssd_bwd", "ssd_materialize_L",
-           "ssd_decay_chunk", "ssd_status_string", "ssd_abi_version")
+           "ssd_decay_chunk", "ssd_status_string", "ssd_abi_version",
+           "ssd_trapezoidal_fwd", "ssd_trapezoidal_bwd_workspace", "ssd_trapezoidal_bwd", "ssd_rope_fwd",
+           "ssd_rope_bwd")
 
 _lib = None
 
@@ -122,6 +124,18 @@ def load():
     lib.ssd_status_string.restype = ctypes.c_char_p
     lib.ssd_abi_version.argtypes = []
     lib.ssd_abi_version.restype = ctypes.c_int
+    # include/ssd_frontend.h
+    i64, i32, sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t
+    lib.ssd_trapezoidal_fwd.argtypes = [i32, i64, i64] + [_vp] * 8 + [_vp]
+    lib.ssd_trapezoidal_fwd.restype = ctypes.c_int
+    lib.ssd_trapezoidal_bwd_workspace.argtypes = [i64, i64]
+    lib.ssd_trapezoidal_bwd_workspace.restype = sz
+    lib.ssd_trapezoidal_bwd.argtypes = [i32, i64, i64] + [_vp] * 12 + [_vp, sz, _vp]
+    lib.ssd_trapezoidal_bwd.restype = ctypes.c_int
+    lib.ssd_rope_fwd.argtypes = [i32, i32, i64, i64, i64, i64, i32, _vp, _vp, _vp, _vp]
+    lib.ssd_rope_fwd.restype = ctypes.c_int
+    lib.ssd_rope_bwd.argtypes = [i32, i32, i64, i64, i64, i64, i32, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.ssd_rope_bwd.restype = ctypes.c_int
     if lib.ssd_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH}: ABI {lib.ssd_abi_version()} != {ABI_VERSION}; rebuild")
     _lib = lib

@@ -13,6 +13,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "ssd_mi355x.h"
+HEADERS = (HEADER, ROOT / "include" / "ssd_frontend.h")
 
 
 @pytest.fixture(scope="module")
@@ -23,7 +24,7 @@ def capi():
 
 
 def _header_functions():
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(ssd_\w+)\s*\(", text, re.M)))
 
 
