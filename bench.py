@@ -328,6 +328,53 @@ def time_trapezoidal(steps=10, warmup=3):
             "fused_drop_over_two_calls": round(res["fused_drop_beta_dA_ms"] / res["two_calls_ms"], 3)}
 
 
+LMHEAD = dict(rows=4 * 4096, vocab=50304, d_model=1024)
+
+
+def time_lmhead(steps=5, warmup=2):
+    """Config 4's loss head: fused LM head + cross-entropy fwd+bwd (bf16 hidden and tied weight,
+    one backward chunk of 4096 rows at a time), with the MFMA roofline of its 8 M V d FLOPs (forward
+    tile product, its recomputation in the backward, and the two gradient GEMMs); beside it the
+    unfused torch composition (bf16 GEMM to fp32 logits, cross_entropy)."""
+    import torch
+    import torch.nn.functional as F
+    import kernels
+
+    dev = torch.device("cuda", 0)
+    M, V, D = LMHEAD["rows"], LMHEAD["vocab"], LMHEAD["d_model"]
+    g = torch.Generator(device=dev).manual_seed(7)
+    h = torch.randn(M, D, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, D, generator=g, device=dev) / D ** 0.5).to(torch.bfloat16).requires_grad_(True)
+    t = torch.randint(0, V, (M,), generator=g, device=dev)
+
+    def fused():
+        kernels.fused_lmhead_xent(h, w, t).backward()
+
+    def unfused():
+        F.cross_entropy((h @ w.t()).float(), t).backward()
+
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, fn in (("fused_ms", fused), ("torch_unfused_ms", unfused)):
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) / steps, 4)
+        h.grad = None
+        w.grad = None
+    flops = 8.0 * M * V * D
+    tf = flops / (res["fused_ms"] * 1e-3) / 1e12
+    return {"workload": f"config 4 loss head: M={M} rows, V={V}, d={D}, bf16, fwd+bwd", **res,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4), "algorithmic_flops": flops}}
+
+
 def kernel_roofline(name, ms, models):
     """Roofline entry of one phase: HBM-bound below the ridge, MFMA-bound above."""
     flops, nbytes = models.get(name, (0, 0))
@@ -423,6 +470,7 @@ def main():
                     help="BASELINE config to time (2 = the headline shape)")
     ap.add_argument("--no-trapezoidal", action="store_true",
                     help="skip the trapezoidal block line (config 4's layer, two calls vs the fused op)")
+    ap.add_argument("--no-lmhead", action="store_true", help="skip the loss-head line (config 4's LM head)")
     a = ap.parse_args()
     global CFG, CFG_ID
     CFG, CFG_ID = dict(CONFIGS[a.config]), a.config
@@ -449,6 +497,8 @@ def main():
     }
     if rank == 0 and not a.no_trapezoidal and CFG_ID == 2:
         out["trapezoidal_block"] = time_trapezoidal()
+    if rank == 0 and not a.no_lmhead and CFG_ID == 2:
+        out["lmhead"] = time_lmhead()
     if rank == 0 and not a.no_cpu_baseline and CFG_ID == 2:
         out["cpu_baseline"] = cpu_baseline()
     if rank == 0:

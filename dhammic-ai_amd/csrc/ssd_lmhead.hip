@@ -1,0 +1,256 @@
+// Fused LM head + cross-entropy (gfx950): logits = hidden W^T on bf16 MFMA, consumed in registers
+// (r2/dhammic-ai/src/kernels/lmhead_xent.py:1-45 for the math). The (M, V) logits never exist:
+//   forward: per 128 x 128 (row, vocab) tile, the row-wise max and sum of exp of the tile's logits
+//            (a partial of the online logsumexp) and the target logit; k_lmhead_combine merges the
+//            partials of a row into logZ;
+//   backward: the same tile product again, then dlogits = (softmax - onehot) * scale * mask written
+//            transposed in bf16 for one chunk of rows, which two library GEMMs turn into d_hidden and
+//            d_weight.
+// The tile product: 4 waves, each a 64 x 64 quarter as 2 x 2 units of v_mfma_f32_32x32x16_bf16
+// (acc[v][r]: rows of the accumulator are vocab entries, lanes are hidden rows, so a row's logits
+// sit in one lane pair and its max / sum need one cross-half exchange); K in steps of 32 through
+// LDS, the next step's tiles loaded into registers while one step computes. Blocks are grouped so
+// that the blocks an XCD runs together share 8 row tiles (2 MB of hidden) while they stream the
+// vocabulary: each weight tile then comes from HBM once per group instead of once per row tile.
+#include "ssd_launch.h"
+#include "ssd_lmhead.h"
+#include "ssd_mi355x.h"
+#include "ssd_tile.h"
+
+namespace {
+
+constexpr int kTR = 128, kTV = 128, kTK = 32;  // rows, vocab entries, K step of a tile
+constexpr int kGroupR = 8;                     // row tiles per group
+
+struct LmArgs {
+  int64_t M, V, row0, rows, ignore, ldg;
+  int d, n_rt, n_vt;
+  const bf16* H;
+  const bf16* W;
+  const int64_t* tgt;
+  float* part_m;   // [M][n_vt] forward partials
+  float* part_s;
+  float* tlogit;   // [M]
+  const float* logZ;
+  const float* scale;
+  bf16* G;         // [V][ldg] backward
+};
+
+__device__ __forceinline__ int64_t eff_target(int64_t t, int64_t ignore, int64_t V, bool& valid) {
+  valid = t != ignore;
+  return (valid && t >= 0 && t < V) ? t : 0;  // lmhead_xent.py:101-103
+}
+
+}  // namespace
+
+template <bool BWD>
+__global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
+  // grouped, XCD-aware tile order: blocks b = 8 k + x run on XCD x; XCD x takes groups x, x + 8, ...
+  const int b = blockIdx.x, x = b & 7, k = b >> 3;
+  const int per_group = kGroupR * a.n_vt;
+  const int gi = x + 8 * (k / per_group), local = k % per_group;
+  const int rt = gi * kGroupR + local % kGroupR, vt = local / kGroupR;
+  if (rt >= a.n_rt) return;
+  const int64_t r0 = a.row0 + (int64_t)rt * kTR, v0 = (int64_t)vt * kTV;
+  const int nr = (int)min<int64_t>(kTR, a.row0 + a.rows - r0), nv = (int)min<int64_t>(kTV, a.V - v0);
+
+  __shared__ __align__(16) bf16 Hs[tsize<kTR, kTK>()];
+  __shared__ __align__(16) bf16 Ws[tsize<kTV, kTK>()];
+  __shared__ float red[2][2][kTR];
+  const int w = threadIdx.x >> 6, wr = w & 1, wv = w >> 1;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) zero(acc[i][j]);
+  TileStage<kTR, kTK, 256> sh;
+  TileStage<kTV, kTK, 256> sw;
+  const bf16* Hb = a.H + r0 * a.d;
+  const bf16* Wb = a.W + v0 * a.d;
+  tstage_load_v(sh, Hb, a.d, nr, a.d);
+  tstage_load_v(sw, Wb, a.d, nv, a.d);
+  for (int kc = 0; kc < a.d; kc += kTK) {
+    __syncthreads();  // the previous step's LDS reads are done
+    tstage_store(sh, Hs);
+    tstage_store(sw, Ws);
+    __syncthreads();
+    if (kc + kTK < a.d) {
+      tstage_load_v(sh, Hb + kc + kTK, a.d, nr, a.d - kc - kTK);
+      tstage_load_v(sw, Wb + kc + kTK, a.d, nv, a.d - kc - kTK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      bf16x8 hf[2], wf[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        hf[u] = tld8<kTK>(Hs, 64 * wr + 32 * u + l32, 16 * ks + 8 * hh);
+        wf[u] = tld8<kTK>(Ws, 64 * wv + 32 * u + l32, 16 * ks + 8 * hh);
+      }
+#pragma unroll
+      for (int uv = 0; uv < 2; ++uv)
+#pragma unroll
+        for (int ur = 0; ur < 2; ++ur) mfma(acc[uv][ur], wf[uv], hf[ur]);
+    }
+  }
+
+  // acc[uv][ur][i]: logit of row r0 + 64 wr + 32 ur + l32 and vocab entry v0 + 64 wv + 32 uv + acc_row(i, lane)
+#pragma unroll
+  for (int ur = 0; ur < 2; ++ur) {
+    const int rl = 64 * wr + 32 * ur + l32;
+    const bool rok = rl < nr;
+    const int64_t r = r0 + rl;
+    bool valid = false;
+    const int64_t te = rok ? eff_target(a.tgt[r], a.ignore, a.V, valid) : -1;
+    if constexpr (!BWD) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int uv = 0; uv < 2; ++uv)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (64 * wv + 32 * uv + acc_row(i, lane) < nv) mx = fmaxf(mx, acc[uv][ur][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mx2 = mx * SSD_LOG2E;
+      float s = 0.0f;
+#pragma unroll
+      for (int uv = 0; uv < 2; ++uv)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int vl = 64 * wv + 32 * uv + acc_row(i, lane);
+          if (vl < nv) {
+            s += exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -mx2));
+            if (v0 + vl == te) a.tlogit[r] = acc[uv][ur][i];  // one lane of the grid holds it
+          }
+        }
+      s += __shfl_xor(s, 32, 64);
+      if (hh == 0) {
+        red[0][wv][rl] = mx;
+        red[1][wv][rl] = s;
+      }
+    } else {
+      if (!rok) continue;
+      const float lz2 = a.logZ[r] * SSD_LOG2E;
+      const float sc = valid ? a.scale[0] : 0.0f;
+      bf16* g = a.G + (r - a.row0);
+#pragma unroll
+      for (int uv = 0; uv < 2; ++uv)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int vl = 64 * wv + 32 * uv + acc_row(i, lane);
+          if (vl < nv) {
+            const float p = exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -lz2));
+            g[(v0 + vl) * a.ldg] = (bf16)((p - (v0 + vl == te ? 1.0f : 0.0f)) * sc);
+          }
+        }
+    }
+  }
+  if constexpr (!BWD) {
+    // the two vocab halves of the tile, then one partial per (row, tile)
+    __syncthreads();
+    if (threadIdx.x < kTR && (int)threadIdx.x < nr) {
+      const int rl = threadIdx.x;
+      const float m0 = red[0][0][rl], m1 = red[0][1][rl];
+      const float m = fmaxf(m0, m1);
+      const float s = red[1][0][rl] * exp2_fast((m0 - m) * SSD_LOG2E) + red[1][1][rl] * exp2_fast((m1 - m) * SSD_LOG2E);
+      const int64_t o = (r0 + rl) * a.n_vt + vt;
+      a.part_m[o] = m;
+      a.part_s[o] = s;
+    }
+  }
+}
+
+// logZ of each row from its n_vt tile partials (one wave per row), and the mask.
+__global__ void __launch_bounds__(256) k_lmhead_combine(int64_t M, int n_vt, const float* __restrict__ part_m,
+                                                        const float* __restrict__ part_s,
+                                                        const int64_t* __restrict__ tgt, int64_t ignore,
+                                                        float* __restrict__ logZ, int32_t* __restrict__ mask) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;
+  const float* pm = part_m + r * n_vt;
+  const float* ps = part_s + r * n_vt;
+  float m = -INFINITY;
+  for (int t = lane; t < n_vt; t += 64) m = fmaxf(m, pm[t]);
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float s = 0.0f;
+  for (int t = lane; t < n_vt; t += 64) s += ps[t] * exp2_fast((pm[t] - m) * SSD_LOG2E);
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0) {
+    logZ[r] = m + logf(s);
+    mask[r] = tgt[r] != ignore ? 1 : 0;
+  }
+}
+
+namespace {
+
+int lm_check(int64_t M, int64_t V, int64_t d, const void* H, const void* W, const int64_t* tgt) {
+  if (M < 1 || V < 1 || d < 1 || !H || !W || !tgt) return SSD_ERR_INVALID;
+  if (d % 8 || (reinterpret_cast<uintptr_t>(H) & 15) || (reinterpret_cast<uintptr_t>(W) & 15))
+    return SSD_ERR_UNSUPPORTED;  // 16-byte rows
+  // buffer offsets of one tile (128 rows of d bf16) stay far below 2 GB; grid and indices in int
+  if (d > (1 << 20) || M > ((int64_t)1 << 40) || V > ((int64_t)1 << 30)) return SSD_ERR_UNSUPPORTED;
+  return SSD_OK;
+}
+
+unsigned lm_blocks(int n_rt, int n_vt) {
+  const int64_t groups = (n_rt + kGroupR - 1) / kGroupR;
+  return (unsigned)(8 * ((groups + 7) / 8) * kGroupR * n_vt);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ssd_lmhead_xent_workspace(int64_t M, int64_t V) {
+  if (M < 1 || V < 1) return 0;
+  return (size_t)(2 * M * ((V + kTV - 1) / kTV)) * sizeof(float);
+}
+
+int ssd_lmhead_xent_fwd(int64_t M, int64_t V, int64_t d, const void* hidden, const void* weight,
+                        const int64_t* targets, int64_t ignore_index, float* logZ, float* target_logit,
+                        int32_t* mask, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = lm_check(M, V, d, hidden, weight, targets);
+  if (st != SSD_OK) return st;
+  if (!logZ || !target_logit || !mask) return SSD_ERR_INVALID;
+  if (!workspace || workspace_bytes < ssd_lmhead_xent_workspace(M, V)) return SSD_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  LmArgs a{};
+  a.M = M; a.V = V; a.row0 = 0; a.rows = M; a.ignore = ignore_index; a.d = (int)d;
+  a.n_rt = (int)((M + kTR - 1) / kTR);
+  a.n_vt = (int)((V + kTV - 1) / kTV);
+  a.H = static_cast<const bf16*>(hidden);
+  a.W = static_cast<const bf16*>(weight);
+  a.tgt = targets;
+  a.part_m = static_cast<float*>(workspace);
+  a.part_s = a.part_m + M * a.n_vt;
+  a.tlogit = target_logit;
+  hipLaunchKernelGGL(k_lmhead<false>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return SSD_ERR_HIP;
+  hipLaunchKernelGGL(k_lmhead_combine, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, M, a.n_vt, a.part_m,
+                     a.part_s, targets, ignore_index, logZ, mask);
+  return hipGetLastError() == hipSuccess ? SSD_OK : SSD_ERR_HIP;
+}
+
+int ssd_lmhead_xent_dlogits(int64_t M, int64_t V, int64_t d, int64_t row0, int64_t rows, const void* hidden,
+                            const void* weight, const int64_t* targets, int64_t ignore_index, const float* logZ,
+                            const float* scale, void* G, int64_t ldg, void* stream) {
+  int st = lm_check(M, V, d, hidden, weight, targets);
+  if (st != SSD_OK) return st;
+  if (!logZ || !scale || !G || row0 < 0 || rows < 1 || row0 + rows > M || ldg < rows) return SSD_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  LmArgs a{};
+  a.M = M; a.V = V; a.row0 = row0; a.rows = rows; a.ignore = ignore_index; a.ldg = ldg; a.d = (int)d;
+  a.n_rt = (int)((rows + kTR - 1) / kTR);
+  a.n_vt = (int)((V + kTV - 1) / kTV);
+  a.H = static_cast<const bf16*>(hidden);
+  a.W = static_cast<const bf16*>(weight);
+  a.tgt = targets;
+  a.logZ = logZ;
+  a.scale = scale;
+  a.G = static_cast<bf16*>(G);
+  hipLaunchKernelGGL(k_lmhead<true>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? SSD_OK : SSD_ERR_HIP;
+}
+
+}  // extern "C"

@@ -87,11 +87,11 @@ class SsdBwdArgs(ctypes.Structure):
     ]
 
 
-# Every symbol include/ssd_mi355x.h and include/ssd_frontend.h declare.
+# Every symbol include/ssd_mi355x.h, include/ssd_frontend.h and include/ssd_lmhead.h declare.
 EXPORTS = ("ssd_validate", "ssd_workspace_bytes", "ssd_fwd", "ssd_fwd_noalloc", "ssd_bwd", "ssd_materialize_L",
            "ssd_decay_chunk", "ssd_status_string", "ssd_abi_version",
            "ssd_trapezoidal_fwd", "ssd_trapezoidal_bwd_workspace", "ssd_trapezoidal_bwd", "ssd_rope_fwd",
-           "ssd_rope_bwd")
+           "ssd_rope_bwd", "ssd_lmhead_xent_workspace", "ssd_lmhead_xent_fwd", "ssd_lmhead_xent_dlogits")
 
 _lib = None
 
@@ -136,6 +136,13 @@ def load():
     lib.ssd_rope_fwd.restype = ctypes.c_int
     lib.ssd_rope_bwd.argtypes = [i32, i32, i64, i64, i64, i64, i32, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.ssd_rope_bwd.restype = ctypes.c_int
+    # include/ssd_lmhead.h
+    lib.ssd_lmhead_xent_workspace.argtypes = [i64, i64]
+    lib.ssd_lmhead_xent_workspace.restype = sz
+    lib.ssd_lmhead_xent_fwd.argtypes = [i64, i64, i64, _vp, _vp, _vp, i64, _vp, _vp, _vp, _vp, sz, _vp]
+    lib.ssd_lmhead_xent_fwd.restype = ctypes.c_int
+    lib.ssd_lmhead_xent_dlogits.argtypes = [i64, i64, i64, i64, i64, _vp, _vp, _vp, i64, _vp, _vp, _vp, i64, _vp]
+    lib.ssd_lmhead_xent_dlogits.restype = ctypes.c_int
     if lib.ssd_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH}: ABI {lib.ssd_abi_version()} != {ABI_VERSION}; rebuild")
     _lib = lib

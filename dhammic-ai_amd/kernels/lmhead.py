@@ -1,0 +1,175 @@
+"""Fused LM head + cross-entropy on MI355X (no (M, V) logits).
+
+Drop-ins for ``fused_lmhead_xent`` / ``FusedLMHeadXent`` / ``FusedLMHeadXentModule``
+(r2/dhammic-ai/src/kernels/lmhead_xent.py:256-431) and ``ChunkedLMHeadXent``
+(r2/dhammic-ai/src/runtime/chunked_lmhead.py:288-431): same arguments, scalar fp32 mean loss
+over the non-ignored targets, gradients for hidden and the (tied) weight.
+
+Device work (include/ssd_lmhead.h): the forward kernel multiplies hidden and weight tiles on bf16
+MFMA and keeps only each row's running max / sum of exp and its target logit; the backward kernel
+recomputes the tiles and writes the logits gradient (softmax - onehot) * dloss / n_valid for one
+chunk of rows in bf16, from which d_hidden = G^T W and d_weight += G hidden are library GEMMs
+(hipBLASLt through torch). The scale dloss / n_valid stays on the device (the reference reads it
+back to the host, lmhead_xent.py:330). bf16 hidden and weight only (the block's dtype); other
+dtypes raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import math
+from typing import Iterable, Union
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import _capi as C_
+from .ssd_scan import _p, _stream
+
+__all__ = ["fused_lmhead_xent", "FusedLMHeadXent", "FusedLMHeadXentModule", "ChunkedLMHeadXent"]
+
+# rows per backward chunk: bounds the bf16 logits-gradient buffer to V x 4096 x 2 bytes
+_BWD_ROWS = 4096
+
+
+class FusedLMHeadXent(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden: Tensor, weight: Tensor, targets: Tensor, ignore_index: int = -100,
+                bwd_rows: int = _BWD_ROWS) -> Tensor:
+        assert hidden.is_cuda and weight.is_cuda and targets.is_cuda, "FusedLMHeadXent requires CUDA tensors"
+        assert weight.dim() == 2, f"weight must be 2-D (V, d), got {tuple(weight.shape)}"
+        assert hidden.shape[-1] == weight.shape[-1], (
+            f"hidden last dim {hidden.shape[-1]} != weight last dim {weight.shape[-1]}")
+        assert targets.dtype == torch.long, f"targets must be int64, got {targets.dtype}"
+        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+            raise NotImplementedError("fused_lmhead_xent: bf16 hidden and weight only")
+        D, V = hidden.shape[-1], weight.shape[0]
+        h = hidden.contiguous().view(-1, D)
+        w = weight.contiguous()
+        t = targets.contiguous().view(-1)
+        M = h.shape[0]
+        assert t.shape[0] == M, f"targets length {t.shape[0]} != hidden rows {M}"
+        dev = h.device
+        logZ = torch.empty(M, dtype=torch.float32, device=dev)
+        tl = torch.empty(M, dtype=torch.float32, device=dev)
+        mask = torch.empty(M, dtype=torch.int32, device=dev)
+        lib = C_.load()
+        ws = torch.empty(lib.ssd_lmhead_xent_workspace(M, V), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            st = lib.ssd_lmhead_xent_fwd(M, V, D, _p(h), _p(w), _p(t), int(ignore_index), _p(logZ), _p(tl), _p(mask),
+                                         _p(ws), ws.numel(), _stream(dev))
+        C_.check(st, "ssd_lmhead_xent_fwd")
+        maskf = mask.to(torch.float32)
+        n_valid = maskf.sum().clamp_min(1.0)
+        loss = ((logZ - tl) * maskf).sum() / n_valid
+        ctx.save_for_backward(h, w, t, logZ, n_valid)
+        ctx.ignore_index = int(ignore_index)
+        ctx.shape = hidden.shape
+        ctx.bwd_rows = int(bwd_rows)
+        return loss
+
+    @staticmethod
+    def backward(ctx, dloss: Tensor):
+        h, w, t, logZ, n_valid = ctx.saved_tensors
+        M, D = h.shape
+        V = w.shape[0]
+        dev = h.device
+        scale = (dloss.detach().to(torch.float32) / n_valid).reshape(1).contiguous()
+        rows = min(M, ctx.bwd_rows)
+        G = torch.empty(V, rows, dtype=torch.bfloat16, device=dev)
+        dh = torch.empty_like(h)
+        dw32 = None
+        dw = None
+        lib = C_.load()
+        for r0 in range(0, M, rows):
+            n = min(rows, M - r0)
+            with torch.cuda.device(dev):
+                st = lib.ssd_lmhead_xent_dlogits(M, V, D, r0, n, _p(h), _p(w), _p(t), ctx.ignore_index, _p(logZ),
+                                                 _p(scale), _p(G), rows, _stream(dev))
+            C_.check(st, "ssd_lmhead_xent_dlogits")
+            g = G[:, :n]
+            dh[r0:r0 + n] = torch.mm(g.t(), w)
+            part = torch.mm(g, h[r0:r0 + n])
+            if r0 == 0 and n == M:
+                dw = part
+            else:
+                dw32 = part.float() if dw32 is None else dw32.add_(part.float())
+        if dw is None:
+            dw = dw32.to(w.dtype)
+        return dh.view(ctx.shape), dw, None, None, None
+
+
+def fused_lmhead_xent(hidden: Tensor, weight: Tensor, targets: Tensor, ignore_index: int = -100) -> Tensor:
+    """Mean cross-entropy of (hidden @ weight.T) against targets, without the (M, V) logits."""
+    return FusedLMHeadXent.apply(hidden, weight, targets, ignore_index)
+
+
+class FusedLMHeadXentModule(nn.Module):
+    """Drop-in fused LM-head + cross-entropy module; a given ``weight`` is shared (weight tying)."""
+
+    def __init__(self, d_model: int, vocab_size: int, weight: nn.Parameter | None = None, ignore_index: int = -100):
+        super().__init__()
+        self.d_model = d_model
+        self.vocab_size = vocab_size
+        self.ignore_index = ignore_index
+        if weight is None:
+            self.weight = nn.Parameter(torch.empty(vocab_size, d_model).normal_(mean=0.0, std=1.0 / math.sqrt(d_model)))
+        else:
+            assert weight.shape == (vocab_size, d_model), (
+                f"tied weight shape {tuple(weight.shape)} != ({vocab_size}, {d_model})")
+            self.weight = weight
+
+    def forward(self, hidden: Tensor, targets: Tensor) -> Tensor:
+        return fused_lmhead_xent(hidden, self.weight, targets, self.ignore_index)
+
+    def extra_repr(self) -> str:
+        return f"d_model={self.d_model}, vocab_size={self.vocab_size}, ignore_index={self.ignore_index}"
+
+
+class ChunkedLMHeadXent(nn.Module):
+    """Sequence-chunked LM head (chunked_lmhead.py:288-431): the token-weighted mean loss over all
+    non-ignored positions of a (B, T, D) tensor, or of an iterable of (B, chunk, D) chunks with
+    matching target chunks. With a tensor, the backward's logits gradient is built for
+    ``chunk_size * B`` rows at a time."""
+
+    def __init__(self, d_model: int, vocab_size: int, weight: nn.Parameter | None = None, chunk_size: int = 256,
+                 ignore_index: int = -100) -> None:
+        super().__init__()
+        if chunk_size <= 0:
+            raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+        self.d_model = d_model
+        self.vocab_size = vocab_size
+        self.chunk_size = chunk_size
+        self.ignore_index = ignore_index
+        if weight is None:
+            self.weight = nn.Parameter(torch.empty(vocab_size, d_model).normal_(mean=0.0, std=1.0 / math.sqrt(d_model)))
+        else:
+            if tuple(weight.shape) != (vocab_size, d_model):
+                raise ValueError(f"tied weight shape {tuple(weight.shape)} != ({vocab_size}, {d_model})")
+            self.weight = weight
+
+    def forward(self, hidden: Union[Tensor, Iterable[Tensor]], targets: Union[Tensor, Iterable[Tensor]],
+                total_tokens: int | None = None) -> Tensor:
+        weight = self.weight
+        if not weight.is_cuda:
+            raise RuntimeError(f"ChunkedLMHeadXent requires a CUDA weight; got {weight.device}.")
+        if isinstance(hidden, Tensor) != isinstance(targets, Tensor):
+            raise TypeError("hidden and targets must both be tensors or both be iterables, got "
+                            f"{type(hidden).__name__} and {type(targets).__name__}")
+        if isinstance(hidden, Tensor):
+            B = hidden.shape[0] if hidden.dim() == 3 else 1
+            return FusedLMHeadXent.apply(hidden.to(weight.device), weight, targets.to(weight.device),
+                                         self.ignore_index, max(1, self.chunk_size * B))
+        pairs = [(h.to(weight.device), t.to(weight.device)) for h, t in zip(hidden, targets)]
+        if not pairs:
+            return weight.sum() * 0.0
+        counts = [(t != self.ignore_index).sum() for _, t in pairs]
+        total = torch.stack(counts).sum().clamp_min(1).to(torch.float32)
+        loss = None
+        for (h, t), n in zip(pairs, counts):
+            part = fused_lmhead_xent(h, weight, t, self.ignore_index) * n.to(torch.float32)
+            loss = part if loss is None else loss + part
+        return loss / total
+
+    def extra_repr(self) -> str:
+        return (f"d_model={self.d_model}, vocab_size={self.vocab_size}, chunk_size={self.chunk_size}, "
+                f"ignore_index={self.ignore_index}")

@@ -1,0 +1,51 @@
+/*
+ * ssd_lmhead.h — C ABI of the MI355X (gfx950) fused LM head + cross-entropy:
+ * logits = hidden W^T, log-softmax and NLL without materialising the (M, V)
+ * logits. Replaces the device work of
+ *   fused_lmhead_xent / FusedLMHeadXent   r2/dhammic-ai/src/kernels/lmhead_xent.py:1-45 (math),
+ *                                          forward kernel :75-140, autograd :256-367, API :367-396
+ *   ChunkedLMHeadXent                     r2/dhammic-ai/src/runtime/chunked_lmhead.py:1-40, :288-431
+ *                                          (the backward's row chunks bound the gradient buffer)
+ *
+ * hidden (M, d) and weight (V, d) are bf16, row-major (d % 8 == 0, 16-byte
+ * aligned rows); products on bf16 MFMA with fp32 accumulation (the reference's
+ * kernel multiplies the same bf16 values in fp32). targets (M,) int64;
+ * ignore_index rows are masked; a target outside [0, V) that is not ignored
+ * reads logit 0, as the reference's clamp does (:101-103).
+ *
+ * Forward: ssd_lmhead_xent_fwd writes per row logZ = logsumexp_v(logits),
+ * the target logit and the mask (the reference's per-row outputs, :99-100);
+ * the mean loss is sum((logZ - target_logit) * mask) / max(sum(mask), 1).
+ * Backward, per chunk of rows [row0, row0 + rows): ssd_lmhead_xent_dlogits writes
+ *   G[v][r - row0] = (exp(logit[r][v] - logZ[r]) - [v == target[r]]) * scale * mask[r]   (bf16)
+ * with the scale read from device memory (dloss / n_valid: no host sync), after
+ * which d_hidden[chunk] = G^T W and d_weight += G hidden[chunk] are two plain
+ * library GEMMs. No allocation inside; stateless; status codes of ssd_mi355x.h.
+ */
+#ifndef SSD_LMHEAD_H
+#define SSD_LMHEAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Workspace bytes of ssd_lmhead_xent_fwd (per (row, vocab tile) partial max and sum). */
+size_t ssd_lmhead_xent_workspace(int64_t M, int64_t V);
+
+int ssd_lmhead_xent_fwd(int64_t M, int64_t V, int64_t d, const void* hidden, const void* weight,
+                        const int64_t* targets, int64_t ignore_index, float* logZ, float* target_logit,
+                        int32_t* mask, void* workspace, size_t workspace_bytes, void* stream);
+
+/* G has leading dimension ldg >= rows (elements); rows <= M - row0. */
+int ssd_lmhead_xent_dlogits(int64_t M, int64_t V, int64_t d, int64_t row0, int64_t rows, const void* hidden,
+                            const void* weight, const int64_t* targets, int64_t ignore_index, const float* logZ,
+                            const float* scale, void* G, int64_t ldg, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSD_LMHEAD_H */

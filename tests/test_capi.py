@@ -13,7 +13,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "ssd_mi355x.h"
-HEADERS = (HEADER, ROOT / "include" / "ssd_frontend.h")
+HEADERS = (HEADER, ROOT / "include" / "ssd_frontend.h", ROOT / "include" / "ssd_lmhead.h")
 
 
 @pytest.fixture(scope="module")

@@ -1,0 +1,92 @@
+"""GPU parity of the fused LM head + cross-entropy (include/ssd_lmhead.h, kernels/lmhead.py)
+against oracle/lmhead.py (pinned on the CPU by torch's cross_entropy) in fp32 on the same bf16
+values: the loss within 1e-5 relative (the products are exact in fp32; only the summation order
+differs), d_hidden and d_weight within 1e-2 normwise (bf16 outputs, as the reference casts them).
+
+Cases: config 4's head (M = 4 x 4096 rows, vocab 50 304, d 1024, tied weight) in one backward chunk
+and in several; odd sizes with ignored rows and an out-of-range target; the chunked-sequence module
+with a tensor and with an iterable of chunks."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from oracle.lmhead import lmhead_xent
+from ssd_testlib import rel_err
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not gpu_available(), reason="needs an MI355X (HIP device)")]
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _fp32_matmul():
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+    torch.backends.cuda.matmul.allow_tf32 = prev
+    torch.cuda.empty_cache()
+
+
+def _inputs(B, T, V, D, seed=0, ignore_every=0, bad_target=False):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    w = (torch.randn(V, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+    t = torch.randint(0, V, (B, T), generator=g)
+    if ignore_every:
+        t.view(-1)[::ignore_every] = -100
+    if bad_target:
+        t.view(-1)[1] = V + 3
+    return h.to(DEV), w.to(DEV), t.to(DEV)
+
+
+def _check(h, w, t, bwd_rows=None, loss_fn=None):
+    import kernels
+    hl, wl = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    if loss_fn is not None:
+        loss = loss_fn(hl, wl)
+    elif bwd_rows is None:
+        loss = kernels.fused_lmhead_xent(hl, wl, t)
+    else:
+        loss = kernels.FusedLMHeadXent.apply(hl, wl, t, -100, bwd_rows)
+    loss.backward()
+    torch.cuda.synchronize()
+    hr, wr = h.float().requires_grad_(True), w.float().requires_grad_(True)
+    ref = lmhead_xent(hr, wr, t)
+    ref.backward()
+    e_loss = abs(loss.item() - ref.item()) / abs(ref.item())
+    e_h, e_w = rel_err(hl.grad, hr.grad), rel_err(wl.grad, wr.grad)
+    print(f"  loss {loss.item():.6f} ref {ref.item():.6f} rel {e_loss:.1e}; d_hidden {e_h:.1e} d_weight {e_w:.1e}",
+          flush=True)
+    assert loss.dtype == torch.float32 and hl.grad.dtype == h.dtype and wl.grad.dtype == w.dtype
+    assert e_loss <= 1e-5
+    assert e_h <= 1e-2 and e_w <= 1e-2
+
+
+@pytest.mark.parametrize("bwd_rows", [None, 4096], ids=["one_chunk", "four_chunks"])
+def test_config4_head(bwd_rows):
+    h, w, t = _inputs(4, 4096, 50304, 1024, seed=1)
+    _check(h, w, t, bwd_rows=bwd_rows if bwd_rows else 1 << 30)
+
+
+@pytest.mark.parametrize("shape", [(3, 37, 1000, 72), (1, 129, 130, 8), (2, 200, 4097, 136)],
+                         ids=["odd", "tiny_d", "wide"])
+def test_odd_sizes_with_ignored_rows(shape):
+    B, T, V, D = shape
+    h, w, t = _inputs(B, T, V, D, seed=2, ignore_every=5, bad_target=True)
+    _check(h, w, t, bwd_rows=64)
+
+
+def test_chunked_module_tensor_and_iterable():
+    import kernels
+    h, w, t = _inputs(2, 300, 2048, 64, seed=3, ignore_every=9)
+    head = kernels.ChunkedLMHeadXent(64, 2048, weight=torch.nn.Parameter(w.clone()), chunk_size=64)
+    _check(h, w, t, loss_fn=lambda hh, ww: kernels.ChunkedLMHeadXent(64, 2048, weight=ww, chunk_size=64)(hh, t))
+    # iterable of (B, chunk, D) chunks: the token-weighted mean of the chunks' losses
+    chunks = [h[:, s:s + 100] for s in range(0, 300, 100)]
+    tch = [t[:, s:s + 100] for s in range(0, 300, 100)]
+    loss_it = head(chunks, tch)
+    ref = lmhead_xent(h.float(), w.float(), t)
+    assert abs(loss_it.item() - ref.item()) <= 1e-5 * abs(ref.item())
