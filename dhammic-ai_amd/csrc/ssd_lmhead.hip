@@ -1,15 +1,17 @@
 // Fused LM head + cross-entropy (gfx950): logits = hidden W^T on bf16 MFMA, consumed in registers
 // (r2/dhammic-ai/src/kernels/lmhead_xent.py:1-45 for the math). The (M, V) logits never exist:
-//   forward: per 128 x 128 (row, vocab) tile, the row-wise max and sum of exp of the tile's logits
+//   forward: per 128 x 256 (row, vocab) tile, the row-wise max and sum of exp of the tile's logits
 //            (a partial of the online logsumexp) and the target logit; k_lmhead_combine merges the
 //            partials of a row into logZ;
 //   backward: the same tile product again, then dlogits = (softmax - onehot) * scale * mask written
 //            transposed in bf16 for one chunk of rows, which two library GEMMs turn into d_hidden and
 //            d_weight.
-// The tile product: 4 waves, each a 64 x 64 quarter as 2 x 2 units of v_mfma_f32_32x32x16_bf16
-// (acc[v][r]: rows of the accumulator are vocab entries, lanes are hidden rows, so a row's logits
-// sit in one lane pair and its max / sum need one cross-half exchange); K in steps of 32 through
-// LDS, the next step's tiles loaded into registers while one step computes. Blocks are grouped so
+// The tile product: 128 rows x 256 vocab entries per block, 4 waves of 64 x 128 as 2 x 4 units of
+// v_mfma_f32_32x32x16_bf16 (acc[v][r]: rows of the accumulator are vocab entries, lanes are hidden
+// rows, so a row's logits sit in one lane pair and its max / sum need one cross-half exchange;
+// each LDS fragment feeds 2 or 4 MFMAs). K in steps of 64 through two LDS buffers: one step
+// computes while the next one's tiles, loaded into registers a step earlier, are stored to the
+// other buffer; one barrier per step. Blocks are grouped so
 // that the blocks an XCD runs together share 8 row tiles (2 MB of hidden) while they stream the
 // vocabulary: each weight tile then comes from HBM once per group instead of once per row tile.
 #include "ssd_launch.h"
@@ -19,8 +21,10 @@
 
 namespace {
 
-constexpr int kTR = 128, kTV = 128, kTK = 32;  // rows, vocab entries, K step of a tile
+constexpr int kTR = 128, kTV = 256, kTK = 64;  // rows, vocab entries, K step of a tile
+constexpr int kUV = 4;                         // 32-entry vocab units per wave
 constexpr int kGroupR = 8;                     // row tiles per group
+constexpr int kGPitch = kTR + 8;               // LDS pitch (bf16) of the backward's [v][r] gradient tile
 
 struct LmArgs {
   int64_t M, V, row0, rows, ignore, ldg;
@@ -54,48 +58,61 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
   const int64_t r0 = a.row0 + (int64_t)rt * kTR, v0 = (int64_t)vt * kTV;
   const int nr = (int)min<int64_t>(kTR, a.row0 + a.rows - r0), nv = (int)min<int64_t>(kTV, a.V - v0);
 
-  __shared__ __align__(16) bf16 Hs[tsize<kTR, kTK>()];
-  __shared__ __align__(16) bf16 Ws[tsize<kTV, kTK>()];
-  __shared__ float red[2][2][kTR];
+  extern __shared__ __align__(16) unsigned char lm_smem[];
+  bf16* Hs = reinterpret_cast<bf16*>(lm_smem);     // [2][kTR][kTK + 8]
+  bf16* Ws = Hs + 2 * tsize<kTR, kTK>();           // [2][kTV][kTK + 8]
+  float* red = reinterpret_cast<float*>(Ws + 2 * tsize<kTV, kTK>());  // [2 (max, sum)][2 wv][kTR]
   const int w = threadIdx.x >> 6, wr = w & 1, wv = w >> 1;
   const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
 
-  floatx16 acc[2][2];
+  floatx16 acc[kUV][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kUV; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) zero(acc[i][j]);
   TileStage<kTR, kTK, 256> sh;
   TileStage<kTV, kTK, 256> sw;
   const bf16* Hb = a.H + r0 * a.d;
   const bf16* Wb = a.W + v0 * a.d;
+  const int nk = (a.d + kTK - 1) / kTK;
   tstage_load_v(sh, Hb, a.d, nr, a.d);
   tstage_load_v(sw, Wb, a.d, nv, a.d);
-  for (int kc = 0; kc < a.d; kc += kTK) {
-    __syncthreads();  // the previous step's LDS reads are done
-    tstage_store(sh, Hs);
-    tstage_store(sw, Ws);
-    __syncthreads();
-    if (kc + kTK < a.d) {
-      tstage_load_v(sh, Hb + kc + kTK, a.d, nr, a.d - kc - kTK);
-      tstage_load_v(sw, Wb + kc + kTK, a.d, nv, a.d - kc - kTK);
-    }
+  tstage_store(sh, Hs);
+  tstage_store(sw, Ws);
+  if (nk > 1) {
+    tstage_load_v(sh, Hb + kTK, a.d, nr, a.d - kTK);
+    tstage_load_v(sw, Wb + kTK, a.d, nv, a.d - kTK);
+  }
+  __syncthreads();
+  for (int s = 0; s < nk; ++s) {
+    const bf16* hc = Hs + (s & 1) * tsize<kTR, kTK>();
+    const bf16* wc = Ws + (s & 1) * tsize<kTV, kTK>();
 #pragma unroll
     for (int ks = 0; ks < kTK / 16; ++ks) {
-      bf16x8 hf[2], wf[2];
+      bf16x8 hf[2], wf[kUV];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        hf[u] = tld8<kTK>(Hs, 64 * wr + 32 * u + l32, 16 * ks + 8 * hh);
-        wf[u] = tld8<kTK>(Ws, 64 * wv + 32 * u + l32, 16 * ks + 8 * hh);
-      }
+      for (int u = 0; u < 2; ++u) hf[u] = tld8<kTK>(hc, 64 * wr + 32 * u + l32, 16 * ks + 8 * hh);
 #pragma unroll
-      for (int uv = 0; uv < 2; ++uv)
+      for (int u = 0; u < kUV; ++u) wf[u] = tld8<kTK>(wc, 128 * wv + 32 * u + l32, 16 * ks + 8 * hh);
+#pragma unroll
+      for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int ur = 0; ur < 2; ++ur) mfma(acc[uv][ur], wf[uv], hf[ur]);
     }
+    if (s + 1 < nk) {
+      // step s + 1 (in registers since step s - 1) into the other buffer; every wave's reads of
+      // that buffer (step s - 1) ended before the previous barrier
+      tstage_store(sh, Hs + ((s + 1) & 1) * tsize<kTR, kTK>());
+      tstage_store(sw, Ws + ((s + 1) & 1) * tsize<kTV, kTK>());
+      __syncthreads();
+      if (s + 2 < nk) {
+        tstage_load_v(sh, Hb + (s + 2) * kTK, a.d, nr, a.d - (s + 2) * kTK);
+        tstage_load_v(sw, Wb + (s + 2) * kTK, a.d, nv, a.d - (s + 2) * kTK);
+      }
+    }
   }
 
-  // acc[uv][ur][i]: logit of row r0 + 64 wr + 32 ur + l32 and vocab entry v0 + 64 wv + 32 uv + acc_row(i, lane)
+  // acc[uv][ur][i]: logit of row r0 + 64 wr + 32 ur + l32 and vocab entry v0 + 128 wv + 32 uv + acc_row(i, lane)
 #pragma unroll
   for (int ur = 0; ur < 2; ++ur) {
     const int rl = 64 * wr + 32 * ur + l32;
@@ -106,43 +123,60 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
     if constexpr (!BWD) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int uv = 0; uv < 2; ++uv)
+      for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (64 * wv + 32 * uv + acc_row(i, lane) < nv) mx = fmaxf(mx, acc[uv][ur][i]);
+          if (128 * wv + 32 * uv + acc_row(i, lane) < nv) mx = fmaxf(mx, acc[uv][ur][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mx2 = mx * SSD_LOG2E;
-      float s = 0.0f;
+      float sum = 0.0f;
 #pragma unroll
-      for (int uv = 0; uv < 2; ++uv)
+      for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int vl = 64 * wv + 32 * uv + acc_row(i, lane);
+          const int vl = 128 * wv + 32 * uv + acc_row(i, lane);
           if (vl < nv) {
-            s += exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -mx2));
+            sum += exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -mx2));
             if (v0 + vl == te) a.tlogit[r] = acc[uv][ur][i];  // one lane of the grid holds it
           }
         }
-      s += __shfl_xor(s, 32, 64);
+      sum += __shfl_xor(sum, 32, 64);
       if (hh == 0) {
-        red[0][wv][rl] = mx;
-        red[1][wv][rl] = s;
+        red[(0 * 2 + wv) * kTR + rl] = mx;
+        red[(1 * 2 + wv) * kTR + rl] = sum;
       }
     } else {
-      if (!rok) continue;
-      const float lz2 = a.logZ[r] * SSD_LOG2E;
-      const float sc = valid ? a.scale[0] : 0.0f;
-      bf16* g = a.G + (r - a.row0);
+      // the tile's logits gradient into LDS as [v][r] (the K loop's buffers are free once every
+      // wave passed the barrier below), then out as whole 16-byte pieces of G's rows
+      if (ur == 0) __syncthreads();
+      const float lz2 = rok ? a.logZ[r] * SSD_LOG2E : 0.0f;
+      const float sc = (rok && valid) ? a.scale[0] : 0.0f;
+      bf16* gs = reinterpret_cast<bf16*>(lm_smem);
 #pragma unroll
-      for (int uv = 0; uv < 2; ++uv)
+      for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int vl = 64 * wv + 32 * uv + acc_row(i, lane);
-          if (vl < nv) {
-            const float p = exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -lz2));
-            g[(v0 + vl) * a.ldg] = (bf16)((p - (v0 + vl == te ? 1.0f : 0.0f)) * sc);
-          }
+          const int vl = 128 * wv + 32 * uv + acc_row(i, lane);
+          const float p = exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -lz2));
+          gs[vl * kGPitch + rl] = (bf16)((p - (v0 + vl == te ? 1.0f : 0.0f)) * sc);
         }
+    }
+  }
+  if constexpr (BWD) {
+    __syncthreads();
+    const bf16* gs = reinterpret_cast<const bf16*>(lm_smem);
+    bf16* g = a.G + (r0 - a.row0);
+    constexpr int CPR = kTR / 8;  // 16-byte pieces per G row segment
+    for (int id = threadIdx.x; id < kTV * CPR; id += 256) {
+      const int vl = id / CPR, c = (id % CPR) * 8;
+      if (vl >= nv || c >= nr) continue;
+      bf16* dst = g + (v0 + vl) * a.ldg + c;
+      const bf16x8 piece = *reinterpret_cast<const bf16x8*>(gs + vl * kGPitch + c);
+      if (c + 8 <= nr) {
+        *reinterpret_cast<bf16x8*>(dst) = piece;
+      } else {
+        for (int e = 0; e < nr - c; ++e) dst[e] = piece[e];
+      }
     }
   }
   if constexpr (!BWD) {
@@ -150,9 +184,10 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
     __syncthreads();
     if (threadIdx.x < kTR && (int)threadIdx.x < nr) {
       const int rl = threadIdx.x;
-      const float m0 = red[0][0][rl], m1 = red[0][1][rl];
+      const float m0 = red[0 * kTR + rl], m1 = red[1 * kTR + rl];
       const float m = fmaxf(m0, m1);
-      const float s = red[1][0][rl] * exp2_fast((m0 - m) * SSD_LOG2E) + red[1][1][rl] * exp2_fast((m1 - m) * SSD_LOG2E);
+      const float s = red[2 * kTR + rl] * exp2_fast((m0 - m) * SSD_LOG2E) +
+                      red[3 * kTR + rl] * exp2_fast((m1 - m) * SSD_LOG2E);
       const int64_t o = (r0 + rl) * a.n_vt + vt;
       a.part_m[o] = m;
       a.part_s[o] = s;
@@ -193,6 +228,11 @@ int lm_check(int64_t M, int64_t V, int64_t d, const void* H, const void* W, cons
   return SSD_OK;
 }
 
+size_t lm_lds_bytes() {
+  static_assert(kTV * kGPitch <= 2 * (tsize<kTR, kTK>() + tsize<kTV, kTK>()), "gradient tile fits the K buffers");
+  return sizeof(bf16) * 2 * ((size_t)tsize<kTR, kTK>() + (size_t)tsize<kTV, kTK>()) + sizeof(float) * 4 * kTR;
+}
+
 unsigned lm_blocks(int n_rt, int n_vt) {
   const int64_t groups = (n_rt + kGroupR - 1) / kGroupR;
   return (unsigned)(8 * ((groups + 7) / 8) * kGroupR * n_vt);
@@ -225,7 +265,8 @@ int ssd_lmhead_xent_fwd(int64_t M, int64_t V, int64_t d, const void* hidden, con
   a.part_m = static_cast<float*>(workspace);
   a.part_s = a.part_m + M * a.n_vt;
   a.tlogit = target_logit;
-  hipLaunchKernelGGL(k_lmhead<false>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), 0, s, a);
+  ensure_lds(k_lmhead<false>, lm_lds_bytes());
+  hipLaunchKernelGGL(k_lmhead<false>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), lm_lds_bytes(), s, a);
   if (hipGetLastError() != hipSuccess) return SSD_ERR_HIP;
   hipLaunchKernelGGL(k_lmhead_combine, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, M, a.n_vt, a.part_m,
                      a.part_s, targets, ignore_index, logZ, mask);
@@ -238,6 +279,7 @@ int ssd_lmhead_xent_dlogits(int64_t M, int64_t V, int64_t d, int64_t row0, int64
   int st = lm_check(M, V, d, hidden, weight, targets);
   if (st != SSD_OK) return st;
   if (!logZ || !scale || !G || row0 < 0 || rows < 1 || row0 + rows > M || ldg < rows) return SSD_ERR_INVALID;
+  if (ldg % 8 || (reinterpret_cast<uintptr_t>(G) & 15)) return SSD_ERR_UNSUPPORTED;  // 16-byte row pieces
   hipStream_t s = static_cast<hipStream_t>(stream);
   LmArgs a{};
   a.M = M; a.V = V; a.row0 = row0; a.rows = rows; a.ignore = ignore_index; a.ldg = ldg; a.d = (int)d;
@@ -249,7 +291,8 @@ int ssd_lmhead_xent_dlogits(int64_t M, int64_t V, int64_t d, int64_t row0, int64
   a.logZ = logZ;
   a.scale = scale;
   a.G = static_cast<bf16*>(G);
-  hipLaunchKernelGGL(k_lmhead<true>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), 0, s, a);
+  ensure_lds(k_lmhead<true>, lm_lds_bytes());
+  hipLaunchKernelGGL(k_lmhead<true>, dim3(lm_blocks(a.n_rt, a.n_vt)), dim3(256), lm_lds_bytes(), s, a);
   return hipGetLastError() == hipSuccess ? SSD_OK : SSD_ERR_HIP;
 }
 

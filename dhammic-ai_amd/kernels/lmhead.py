@@ -27,14 +27,15 @@ from .ssd_scan import _p, _stream
 
 __all__ = ["fused_lmhead_xent", "FusedLMHeadXent", "FusedLMHeadXentModule", "ChunkedLMHeadXent"]
 
-# rows per backward chunk: bounds the bf16 logits-gradient buffer to V x 4096 x 2 bytes
-_BWD_ROWS = 4096
+# bytes of the backward's bf16 logits-gradient buffer (V x rows); at config 4's head (V = 50 304)
+# 2 GiB holds all 16 384 rows, so one pair of GEMMs produces d_weight without a running sum
+_BWD_BYTES = 2 << 30
 
 
 class FusedLMHeadXent(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden: Tensor, weight: Tensor, targets: Tensor, ignore_index: int = -100,
-                bwd_rows: int = _BWD_ROWS) -> Tensor:
+                bwd_rows: int | None = None) -> Tensor:
         assert hidden.is_cuda and weight.is_cuda and targets.is_cuda, "FusedLMHeadXent requires CUDA tensors"
         assert weight.dim() == 2, f"weight must be 2-D (V, d), got {tuple(weight.shape)}"
         assert hidden.shape[-1] == weight.shape[-1], (
@@ -64,7 +65,7 @@ class FusedLMHeadXent(torch.autograd.Function):
         ctx.save_for_backward(h, w, t, logZ, n_valid)
         ctx.ignore_index = int(ignore_index)
         ctx.shape = hidden.shape
-        ctx.bwd_rows = int(bwd_rows)
+        ctx.bwd_rows = int(bwd_rows) if bwd_rows else max(128, _BWD_BYTES // (2 * V) // 128 * 128)
         return loss
 
     @staticmethod
@@ -75,7 +76,8 @@ class FusedLMHeadXent(torch.autograd.Function):
         dev = h.device
         scale = (dloss.detach().to(torch.float32) / n_valid).reshape(1).contiguous()
         rows = min(M, ctx.bwd_rows)
-        G = torch.empty(V, rows, dtype=torch.bfloat16, device=dev)
+        ldg = (rows + 7) // 8 * 8
+        G = torch.empty(V, ldg, dtype=torch.bfloat16, device=dev)
         dh = torch.empty_like(h)
         dw32 = None
         dw = None
@@ -84,7 +86,7 @@ class FusedLMHeadXent(torch.autograd.Function):
             n = min(rows, M - r0)
             with torch.cuda.device(dev):
                 st = lib.ssd_lmhead_xent_dlogits(M, V, D, r0, n, _p(h), _p(w), _p(t), ctx.ignore_index, _p(logZ),
-                                                 _p(scale), _p(G), rows, _stream(dev))
+                                                 _p(scale), _p(G), ldg, _stream(dev))
             C_.check(st, "ssd_lmhead_xent_dlogits")
             g = G[:, :n]
             dh[r0:r0 + n] = torch.mm(g.t(), w)

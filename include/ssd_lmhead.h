@@ -39,7 +39,7 @@ int ssd_lmhead_xent_fwd(int64_t M, int64_t V, int64_t d, const void* hidden, con
                         const int64_t* targets, int64_t ignore_index, float* logZ, float* target_logit,
                         int32_t* mask, void* workspace, size_t workspace_bytes, void* stream);
 
-/* G has leading dimension ldg >= rows (elements); rows <= M - row0. */
+/* G has leading dimension ldg >= rows (elements, a multiple of 8, G 16-byte aligned); rows <= M - row0. */
 int ssd_lmhead_xent_dlogits(int64_t M, int64_t V, int64_t d, int64_t row0, int64_t rows, const void* hidden,
                             const void* weight, const int64_t* targets, int64_t ignore_index, const float* logZ,
                             const float* scale, void* G, int64_t ldg, void* stream);
