@@ -1,15 +1,17 @@
 // Fused LM head + cross-entropy (gfx950): logits = hidden W^T on bf16 MFMA, consumed in registers
 // (r2/dhammic-ai/src/kernels/lmhead_xent.py:1-45 for the math). The (M, V) logits never exist:
-//   forward: per 128 x 256 (row, vocab) tile, the row-wise max and sum of exp of the tile's logits
+//   forward: per 128 x 128 (row, vocab) tile, the row-wise max and sum of exp of the tile's logits
 //            (a partial of the online logsumexp) and the target logit; k_lmhead_combine merges the
 //            partials of a row into logZ;
 //   backward: the same tile product again, then dlogits = (softmax - onehot) * scale * mask written
 //            transposed in bf16 for one chunk of rows, which two library GEMMs turn into d_hidden and
 //            d_weight.
-// The tile product: 128 rows x 256 vocab entries per block, 4 waves of 64 x 128 as 2 x 4 units of
+// The tile product: 128 rows x 128 vocab entries per block, 4 waves of 64 x 64 as 2 x 2 units of
 // v_mfma_f32_32x32x16_bf16 (acc[v][r]: rows of the accumulator are vocab entries, lanes are hidden
 // rows, so a row's logits sit in one lane pair and its max / sum need one cross-half exchange;
-// each LDS fragment feeds 2 or 4 MFMAs). K in steps of 64 through two LDS buffers: one step
+// each LDS fragment feeds 2 MFMAs). 64 accumulator registers and ~74 KB of LDS per block let two
+// blocks share a CU (two waves per SIMD), which hides the LDS reads behind the other block's MFMAs
+// better than one 128 x 256 block with twice the reuse per fragment. K in steps of 64 through two LDS buffers: one step
 // computes while the next one's tiles, loaded into registers a step earlier, are stored to the
 // other buffer; one barrier per step. Blocks are grouped so
 // that the blocks an XCD runs together share 8 row tiles (2 MB of hidden) while they stream the
@@ -21,8 +23,8 @@
 
 namespace {
 
-constexpr int kTR = 128, kTV = 256, kTK = 64;  // rows, vocab entries, K step of a tile
-constexpr int kUV = 4;                         // 32-entry vocab units per wave
+constexpr int kTR = 128, kTV = 128, kTK = 64;  // rows, vocab entries, K step of a tile
+constexpr int kUV = 2;                         // 32-entry vocab units per wave
 constexpr int kGroupR = 8;                     // row tiles per group
 constexpr int kGPitch = kTR + 8;               // LDS pitch (bf16) of the backward's [v][r] gradient tile
 
@@ -93,7 +95,7 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) hf[u] = tld8<kTK>(hc, 64 * wr + 32 * u + l32, 16 * ks + 8 * hh);
 #pragma unroll
-      for (int u = 0; u < kUV; ++u) wf[u] = tld8<kTK>(wc, 128 * wv + 32 * u + l32, 16 * ks + 8 * hh);
+      for (int u = 0; u < kUV; ++u) wf[u] = tld8<kTK>(wc, 32 * kUV * wv + 32 * u + l32, 16 * ks + 8 * hh);
 #pragma unroll
       for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
@@ -126,7 +128,7 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
       for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (128 * wv + 32 * uv + acc_row(i, lane) < nv) mx = fmaxf(mx, acc[uv][ur][i]);
+          if (32 * kUV * wv + 32 * uv + acc_row(i, lane) < nv) mx = fmaxf(mx, acc[uv][ur][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mx2 = mx * SSD_LOG2E;
       float sum = 0.0f;
@@ -134,7 +136,7 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
       for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int vl = 128 * wv + 32 * uv + acc_row(i, lane);
+          const int vl = 32 * kUV * wv + 32 * uv + acc_row(i, lane);
           if (vl < nv) {
             sum += exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -mx2));
             if (v0 + vl == te) a.tlogit[r] = acc[uv][ur][i];  // one lane of the grid holds it
@@ -156,7 +158,7 @@ __global__ void __launch_bounds__(256) k_lmhead(LmArgs a) {
       for (int uv = 0; uv < kUV; ++uv)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int vl = 128 * wv + 32 * uv + acc_row(i, lane);
+          const int vl = 32 * kUV * wv + 32 * uv + acc_row(i, lane);
           const float p = exp2_fast(fmaf(acc[uv][ur][i], SSD_LOG2E, -lz2));
           gs[vl * kGPitch + rl] = (bf16)((p - (v0 + vl == te ? 1.0f : 0.0f)) * sc);
         }
