@@ -103,56 +103,108 @@ __device__ __forceinline__ void cursor_fetch(const StateCtx& x, Cursor& u) {
   u.ci = x.chunks[u.c];
 }
 
+// The issue cursor: the walk position whose rows the next DMAs fetch, with the bases of its
+// chunk's rows (set when the cursor enters a chunk; a step's rows are then the soffset t * pitch).
+struct IssueCur {
+  int k, t;
+  ChunkInfo ci;
+  const bf16* bu;
+  const bf16* bv;
+  const float* bs;
+};
+
+// Per-wave loop invariants of the ring DMAs. Every wave issues UPW row DMAs of x / dy and VPW of
+// B / C per step (the same split in every wave, so no wave branches on its share), plus one
+// scalar row: wave 0 cs, wave 1 dt (forward, when given), the others a masked one.
+template <int PT>
+struct IssueLanes {
+  using Cfg = StateCfg<PT>;
+  static constexpr int UPW = Cfg::UI / Cfg::NW, VPW = Cfg::VI / Cfg::NW;
+  static_assert(Cfg::UI % Cfg::NW == 0 && Cfg::VI % Cfg::NW == 0, "per-wave DMA split");
+  int ou[UPW], ov[VPW];  // lane's byte offset within the step's rows (SSD_BUF_SIZE: column outside)
+  int lu[UPW], lv[VPW];  // lane's row within the step
+  int os;                // scalar row: lane's byte offset (SSD_BUF_SIZE: this wave loads none)
+  int sstr;              // scalar row: bytes per token
+  bool sdt;              // the scalar row is dt (masked past the step's rows)
+};
+
+template <int PT, bool FWD>
+__device__ __forceinline__ IssueLanes<PT> issue_lanes(const StateCtx& x, int lane) {
+  using Cfg = StateCfg<PT>;
+  using IL = IssueLanes<PT>;
+  constexpr int PP = Cfg::PP, UG = PP / 8, URI = 64 / UG;  // granules per U row, U rows per DMA
+  const SsdDims& d = x.d;
+  IL il;
+#pragma unroll
+  for (int q = 0; q < IL::UPW; ++q) {
+    const int qq = x.w * IL::UPW + q;
+    const int r = qq * URI + lane / UG, gcol = swz_tr<PP>(r, lane % UG) << 3;
+    il.lu[q] = r;
+    il.ou[q] = gcol < d.P ? (int)((r * x.urow + gcol) * 2) : SSD_BUF_SIZE;
+  }
+#pragma unroll
+  for (int q = 0; q < IL::VPW; ++q) {
+    const int vi = x.w * IL::VPW + q;
+    const int r = vi * 8 + lane / 8, gcol = swz_tr<64>(r, lane % 8) << 3;
+    il.lv[q] = r;
+    il.ov[q] = 64 * x.np + gcol < d.N ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE;
+  }
+  il.sdt = FWD && d.has_dt && x.w == 1;
+  il.sstr = il.sdt ? d.H * 4 : 4;
+  il.os = x.w == 0 ? lane * 4 : (il.sdt ? lane * d.H * 4 : SSD_BUF_SIZE);
+  return il;
+}
+
+// Enter the issue cursor's chunk: its table entry and the bases of its rows.
+template <int PT, bool FWD>
+__device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<PT>& il, IssueCur& u) {
+  const SsdDims& d = x.d;
+  const int kc = min(u.k, x.nch - 1);
+  const int c = __builtin_amdgcn_readfirstlane(FWD ? x.c0 + kc : x.c1 - 1 - kc);
+  u.ci = x.chunks[c];
+  u.bu = x.U + (int64_t)u.ci.row0 * x.urow + x.ucol;
+  u.bv = x.V + (int64_t)u.ci.row0 * x.vrow + x.vcol;
+  u.bs = il.sdt ? x.dt + (int64_t)u.ci.row0 * d.H + x.h : x.cs + ((int64_t)c * d.H + x.h) * d.Qpad;
+}
+
 // One step's DMAs into ring slot `nxt`: StateCfg::D per wave, also past the last step
 // (then masked to zeros), so that every step issues the same count. Advances the
 // issue cursor.
 template <int PT, bool FWD>
-__device__ __forceinline__ void state_issue(const StateCtx& x, unsigned char* __restrict__ nxt, Cursor& u, int lane) {
+__device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<PT>& il, unsigned char* __restrict__ nxt,
+                                            IssueCur& u, int lane) {
   using Cfg = StateCfg<PT>;
-  constexpr int PP = Cfg::PP;
-  const SsdDims& d = x.d;
+  using IL = IssueLanes<PT>;
   const bool live = u.k < x.nch;
-  const int c = u.c;
-  const ChunkInfo ci = u.ci;
   const int t0i = live ? u.t : 0;
-  const int nrows = live ? min(64, ci.len - t0i) : 0;
-  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(x.U + (int64_t)(ci.row0 + t0i) * x.urow + x.ucol);
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(x.V + (int64_t)(ci.row0 + t0i) * x.vrow + x.vcol);
-  constexpr int UG = PP / 8, URI = 64 / UG;  // granules per U row, U rows per DMA
+  const int nrows = live ? min(64, u.ci.len - t0i) : 0;
+  const int su = t0i * (int)x.urow * 2, sv = t0i * (int)x.vrow * 2;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(u.bu), rv = buf_rsrc(u.bv), rs = buf_rsrc(u.bs);
+  // (each offset goes through a plain int: an argument whose type depends on the template would
+  // make the target builtin's call dependent, which the host pass cannot resolve)
 #pragma unroll
-  for (int q = 0; q < Cfg::PERW; ++q) {
-    const int qq = x.w * Cfg::PERW + q;
-    if (qq < Cfg::UI) {
-      const int r = qq * URI + lane / UG, j = lane % UG;
-      const int gcol = swz_tr<PP>(r, j) << 3;
-      const bool ok = r < nrows && gcol < d.P;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ru, (__attribute__((address_space(3))) void*)(nxt + qq * 1024), 16,
-                                               ok ? (int)((r * x.urow + gcol) * 2) : SSD_BUF_SIZE, 0, 0, 0);
-    } else {
-      const int vi = qq - Cfg::UI;
-      const int r = vi * 8 + lane / 8, j = lane % 8;
-      const int gcol = swz_tr<64>(r, j) << 3;
-      const bool ok = r < nrows && 64 * x.np + gcol < d.N;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv,
-                                               (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + vi * 1024),
-                                               16, ok ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE, 0, 0, 0);
-    }
-  }
-  // scalar rows: wave 0 cs of the step's tokens, wave 1 dt (forward), the others nothing
-  {
-    const float* csh = x.cs + ((int64_t)c * d.H + x.h) * d.Qpad;
-    const bool dtw = FWD && d.has_dt && x.w == 1;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(dtw ? x.dt + (int64_t)(ci.row0 + t0i) * d.H + x.h : csh);
-    const int off = x.w == 0 ? (t0i + lane) * 4 : (dtw && lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE);
+  for (int q = 0; q < IL::UPW; ++q) {
+    const int vo = il.lu[q] < nrows ? il.ou[q] : SSD_BUF_SIZE;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB + x.w * 256), 4, off, 0, 0, 0);
+        ru, (__attribute__((address_space(3))) void*)(nxt + (x.w * IL::UPW + q) * 1024), 16, vo, su, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < IL::VPW; ++q) {
+    const int vo = il.lv[q] < nrows ? il.ov[q] : SSD_BUF_SIZE;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rv, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + (x.w * IL::VPW + q) * 1024), 16, vo, sv, 0, 0);
+  }
+  {
+    const int vo = (!il.sdt || lane < nrows) ? il.os : SSD_BUF_SIZE, so = t0i * il.sstr;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB + x.w * 256), 4, vo, so, 0, 0);
   }
   if (live) {
     u.t += 64;
-    if (u.t >= ci.len) {
+    if (u.t >= u.ci.len) {
       ++u.k;
       u.t = 0;
-      cursor_fetch<FWD>(x, u);
+      issue_fetch<PT, FWD>(x, il, u);
     }
   }
 }
@@ -165,14 +217,14 @@ template <int PT, bool FWD>
 __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
                                            unsigned char* __restrict__ nxt, float* __restrict__ cw,
                                            bf16* __restrict__ tw, bf16* __restrict__ hbw, float* __restrict__ red,
-                                           Cursor& ui, Cursor& uc, float& tot, int& st, int& s_start,
-                                           floatx16& acc, floatx16& run) {
+                                           const IssueLanes<PT>& il, IssueCur& ui, Cursor& uc, float& tot, int& st,
+                                           int& s_start, floatx16& acc, floatx16& run) {
   using Cfg = StateCfg<PT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
   constexpr bool WIDE = state_wide<PT, FWD>();
   const SsdDims& d = x.d;
   const int lane = threadIdx.x & 63;
-  state_issue<PT, FWD>(x, nxt, ui, lane);
+  state_issue<PT, FWD>(x, il, nxt, ui, lane);
   const int c = uc.c;
   const int clen = uc.ci.len;
   int& t0 = uc.t;
@@ -292,8 +344,9 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   }
 }
 
+// LDS allows two waves per SIMD at every PT (two blocks of 2 PT waves up to PT = 2, one of 8 at PT = 4)
 template <int PT, bool FWD>
-__global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2, 2))) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
                                                          const float* __restrict__ cs, const float* __restrict__ dt,
                                                          const bf16* __restrict__ U, const bf16* __restrict__ V,
@@ -367,23 +420,35 @@ __global__ void __launch_bounds__(128 * PT) k_state_fused(SsdDims d, const Chunk
   x.c1 = seq_chunk0[sq + 1];
   x.nch = x.c1 - x.c0;
 
-  Cursor ui{0, 0, 0, {}}, uc{0, 0, 0, {}};  // issue and compute cursors
-  float tot = 0.0f;                          // total log-decay of the compute cursor's chunk
+  const IssueLanes<PT> il = issue_lanes<PT, FWD>(x, lane);
+  IssueCur ui{};                  // issue cursor
+  Cursor uc{0, 0, 0, {}};         // compute cursor
+  float tot = 0.0f;               // total log-decay of the compute cursor's chunk
   if (x.nch > 0) {  // (an empty sequence passes its state through)
-    cursor_fetch<FWD>(x, ui);
-    uc = ui;
+    issue_fetch<PT, FWD>(x, il, ui);
+    cursor_fetch<FWD>(x, uc);
     tot = cs[((int64_t)uc.c * d.H + x.h) * d.Qpad + d.Qpad - 1];
-    state_issue<PT, FWD>(x, smem, ui, lane);
-    state_issue<PT, FWD>(x, smem + SLOT, ui, lane);
+    state_issue<PT, FWD>(x, il, smem, ui, lane);
+    state_issue<PT, FWD>(x, il, smem + SLOT, ui, lane);
   }
   floatx16 acc;
   zero(acc);
   int st = 0, s_start = 0;  // step count, step of the chunk's start
-  while (uc.k < x.nch) {
+  // step st reads slot st % 3 and refills slot (st + 2) % 3; unrolled three times so that every
+  // slot address is a constant (the LDS reads carry it in their offset field)
+  static_assert(Cfg::R == 3, "three-slot ring");
+  auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
     wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
     lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
-    state_step<PT, FWD>(x, smem + (st % Cfg::R) * SLOT, smem + ((st + 2) % Cfg::R) * SLOT, cw + x.w * 64,
-                        s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, ui, uc, tot, st, s_start, acc, run);
+    state_step<PT, FWD>(x, cur, nxt, cw + x.w * 64, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, il, ui, uc, tot, st,
+                        s_start, acc, run);
+  };
+  while (uc.k < x.nch) {
+    step(smem, smem + 2 * SLOT);
+    if (uc.k >= x.nch) break;
+    step(smem + SLOT, smem);
+    if (uc.k >= x.nch) break;
+    step(smem + 2 * SLOT, smem + SLOT);
   }
   wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
   // final state (forward) / gradient of the initial state (backward)
