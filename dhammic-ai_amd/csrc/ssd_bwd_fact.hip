@@ -301,10 +301,16 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     xt_load<PP, NP>(UR + oD, xt, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
   };
   // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
+  // Run by the dS waves only (threads 0 .. 64 kDsWaves - 1), while the dX waves stage the next head.
+  // (thread offsets come from an opaque thread id recomputed per head: held across the head loop they
+  // spill, and each reload waits for every outstanding load and store of the wave)
+  constexpr int kFl = 64 * kDsWaves;
   auto flush = [&](int h) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     const int64_t hq = ((int64_t)c * d.H + h) * Qpad;
-    if (threadIdx.x < 64) {
-      const int tl = threadIdx.x, tg = 64 * j + tl;
+    if (tid < 64) {
+      const int tl = tid, tg = 64 * j + tl;
       if (tg < ci.len) {
         float cg = 0.0f;
 #pragma unroll
@@ -314,17 +320,17 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         a.xdx[hq + tg] = red_x[tl] + red_x[64 + tl];
       }
     }
-    for (int e = threadIdx.x; e < nt_i * 64; e += kThreads) {
+    for (int e = tid; e < nt_i * 64; e += kFl) {
       const int t = e / 64, l = e % 64;
       const int lg = 64 * (j + t) + l;
       if (lg < ci.len)
         a.rowG[((int64_t)j * d.max_chunks + c) * d.H * (int64_t)Qpad + (int64_t)h * Qpad + lg] =
             red_row[(t * 2 + 0) * 64 + l] + red_row[(t * 2 + 1) * 64 + l];
     }
-    if (threadIdx.x == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_d[0] + red_d[1] + red_d[2] + red_d[3];
+    if (tid == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_d[0] + red_d[1] + red_d[2] + red_d[3];
     constexpr int CPR = PP / 8;
 #pragma unroll
-    for (int id = threadIdx.x; id < 64 * CPR; id += kThreads) {
+    for (int id = tid; id < 64 * CPR; id += kFl) {
       const int r = id / CPR, k = (id % CPR) * 8;
       if (64 * j + r < ci.len && k < d.P && MODE != 2)
         *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + k) =
@@ -361,8 +367,9 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
       // f_l of rows 64 j + xt and v_s of the head's tokens s (block j); zero for a flagged head
       frow[xt] = (ok && xt < 64 * nt_i) ? exp2_fast(hs.fcs * SSD_LOG2E - e_cj2) : 0.0f;
       if (pt == 0 && hh == 0) vrow[32 * sr + l32] = ok ? e_dt * exp2_fast(e_cj2 - e_c2) : 0.0f;
+    } else if (k > 0) {
+      flush(head(k - 1));  // its LDS (ot, reductions) is not touched by the staging above
     }
-    if (k > 0) flush(head(k - 1));  // its LDS (ot, reductions) is not touched by the staging above
     lds_barrier();
 
     if (!xrole) {
