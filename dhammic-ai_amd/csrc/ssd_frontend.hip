@@ -25,7 +25,8 @@ __device__ __forceinline__ float ld0(const T* p, int64_t i) {
   return p ? to_f(p[i]) : 0.0f;
 }
 
-__device__ __forceinline__ float softplus_f(float s) { return fmaxf(s, 0.0f) + log1pf(expf(-fabsf(s))); }
+// the reference kernel's forms (trapezoidal.py:108-113): softplus as max(s, 0) + log(1 + exp(-|s|))
+__device__ __forceinline__ float softplus_f(float s) { return fmaxf(s, 0.0f) + logf(1.0f + expf(-fabsf(s))); }
 __device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 }  // namespace

@@ -19,6 +19,9 @@ SSD so that the comparison runs the reference's own composition:
   non-ignored targets (the fused kernel's chunking over the vocabulary does not change the value).
 * ``trapezoidal`` follows ``src/kernels/trapezoidal.py:1-52``; ``rope`` follows ``src/kernels/rope.py:1-25``;
   ``rmsnorm`` follows ``src/kernels/rmsnorm.py:222-235`` (fp32 statistics, output in the input dtype).
+* ``set_native`` switches the blocks to the native composition (``Mamba3Block.forward_native``: in-projection
+  split, trapezoidal coefficients, RoPE, one trapezoidal scan with D and the gated norm fused, then out_proj)
+  and optionally the loss to the fused LM head, for the tests that check that composition against this one.
 
 The SSD function is a parameter with the reference's public signature
 ``ssd(x, A, B, C, chunk_size, initial_states=None, cache=None) -> (Y, final_state, cache)``, so the same model
@@ -48,10 +51,13 @@ class RMSNorm(nn.Module):
 
 
 def trapezoidal(dt_raw, lam_raw, dt_bias, A_log):
-    """(dt, dA, beta, gamma) in the dtype of dt_raw, computed in fp32."""
-    dt = F.softplus(dt_raw.float() + dt_bias.float())
-    lam = torch.sigmoid(lam_raw.float())
-    A = -torch.exp(A_log.float())
+    """(dt, dA, beta, gamma) in the dtype of dt_raw, computed in fp32 as the reference kernel does: the
+    parameters cast to the input dtype first (trapezoidal.py:241-242), softplus as
+    max(s, 0) + log(1 + exp(-|s|)) (:108-110)."""
+    s = dt_raw.float() + dt_bias.to(dt_raw.dtype).float()
+    dt = torch.clamp_min(s, 0.0) + torch.log(1.0 + torch.exp(-s.abs()))
+    lam = 1.0 / (1.0 + torch.exp(-lam_raw.float()))
+    A = -torch.exp(A_log.to(dt_raw.dtype).float())
     dA = dt * A
     beta = (1.0 - lam) * dt * torch.exp(dA)
     gamma = lam * dt
@@ -86,8 +92,11 @@ class Mamba3Block(nn.Module):
         self.C_bias = nn.Parameter(torch.ones(n_heads, d_state))
         self.out_proj = nn.Linear(self.d_inner, d_model, bias=False, dtype=dtype)
         self.norm = RMSNorm(self.d_inner)
+        self.native = False
 
     def forward(self, x):
+        if self.native:
+            return self.forward_native(x)
         b, T, _ = x.shape
         x = x.to(self.in_proj.weight.dtype)
         z, x_ssm, B_proj, C_proj, dt_raw, lam_raw, theta = torch.split(self.in_proj(x), self.split_sizes, dim=-1)
@@ -114,6 +123,30 @@ class Mamba3Block(nn.Module):
         y = y + x_heads * self.D.to(dtype).view(1, 1, -1, 1)
         y = self.norm(y.reshape(b, T, -1)) * F.silu(z)
         return self.out_proj(y)
+
+    def forward_native(self, x):
+        """The same block on the native kernels: the in-projection split, the trapezoidal coefficients
+        and the RoPE of B/C as HIP kernels, then one trapezoidal scan with + D x and the gated output
+        norm in its last phase (no padding: the last chunk is partial), feeding out_proj."""
+        import kernels
+        b, T, _ = x.shape
+        x = x.to(self.in_proj.weight.dtype)
+        z, x_ssm, B_proj, C_proj, dt_raw, lam_raw, theta = kernels.fused_inproj_split(x, self.in_proj.weight,
+                                                                                     self.split_sizes)
+        dt, dA, beta, gamma = kernels.fused_trapezoidal(dt_raw, lam_raw, self.dt_bias, self.A_log)
+        B_proj = self.B_norm(B_proj)
+        C_proj = self.C_norm(C_proj)
+        cum_angles = -torch.cumsum(dt.unsqueeze(-1) * theta.unsqueeze(2), dim=1)
+        dtype = x_ssm.dtype
+        # rotated in fp32 and rounded after, as the reference does (the bias gradients sum every token's
+        # gradient with heavy cancellation, so a rounding before the rotation shows in them)
+        ang = cum_angles.float()
+        B_h = kernels.fused_rope(B_proj.unsqueeze(2) + self.B_bias, ang).to(dtype)
+        C_h = kernels.fused_rope(C_proj.unsqueeze(2) + self.C_bias, ang).to(dtype)
+        x_heads = x_ssm.reshape(b, T, self.n_heads, self.d_head)
+        y = kernels.fused_trapezoidal_ssd_scan(x_heads, dA, gamma, beta, B_h, C_h, self.chunk_size, D=self.D, z=z,
+                                               norm_weight=self.norm.weight, norm_eps=self.norm.eps)
+        return self.out_proj(y.reshape(b, T, -1))
 
 
 class SwiGLU(nn.Module):
@@ -154,6 +187,7 @@ class Mamba3LM(nn.Module):
             [Layer(ssd, d_model, d_state, expand, n_heads, chunk_size, mlp_hidden, dtype) for _ in range(n_layers)])
         self.norm_f = RMSNorm(d_model, eps=1e-5)
         self.checkpoint = checkpoint
+        self.native_head = False
 
     def loss(self, tokens, targets, ignore_index=-100):
         h = self.embed(tokens)
@@ -163,6 +197,9 @@ class Mamba3LM(nn.Module):
             else:
                 h = layer(h)
         hidden = self.norm_f(h)
+        if self.native_head:
+            import kernels
+            return kernels.fused_lmhead_xent(hidden, self.embed.weight, targets, ignore_index)
         logits = hidden.float() @ self.embed.weight.float().t()
         return F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1), ignore_index=ignore_index)
 
@@ -170,3 +207,11 @@ class Mamba3LM(nn.Module):
 def set_ssd(model, ssd):
     for layer in model.layers:
         layer.mixer.ssd = ssd
+
+
+def set_native(model, blocks, head=False):
+    """Run the blocks on the native kernels end to end (Mamba3Block.forward_native) and, with ``head``,
+    the loss on the fused LM head (bf16 only)."""
+    for layer in model.layers:
+        layer.mixer.native = blocks
+    model.native_head = head

@@ -18,7 +18,13 @@ tokens with the oracle's restatement of the reference SSD.
   multiple), both bf16 with the same criterion.
 
 Every op outside the SSD is shared by the runs (same weights, same ops), so the differences come from the SSD
-alone. The blocks make the reference's two SSD calls per layer (the beta path reusing the gamma path's cache,
+alone.
+
+The native composition (``test_native_composition_*``) runs each block on the native kernels end to end: the
+in-projection split, trapezoidal coefficients and RoPE kernels, one fused trapezoidal scan with D and the gated
+output norm in its last phase feeding out_proj, and in bf16 the fused LM head for the loss. It is checked
+against the reference composition (the block's torch ops around the oracle's two SSD calls) with the same bars:
+fp32 loss 1e-4 and gradients 1e-3; bf16 against the reference's own bf16 deviation. The blocks make the reference's two SSD calls per layer (the beta path reusing the gamma path's cache,
 which drops the beta path's A gradient in both). Layers are checkpointed (recomputed in the backward) in every
 run alike. On the CPU the check fails for a dropped dA gradient and for a beta call that ignores the cache.
 """
@@ -28,7 +34,7 @@ import pytest
 import torch
 
 from conftest import gpu_available
-from model_lib import Mamba3LM, set_ssd
+from model_lib import Mamba3LM, set_native, set_ssd
 from oracle import ssd_chunked as oc
 from ssd_testlib import rel_err
 
@@ -121,6 +127,66 @@ def test_training_step_bf16(sizes, b, T, checkpoint):
     # the native SSD's bf16 arithmetic moves the gradients as much as the reference's own does ...
     assert ratios[len(ratios) // 2] <= 1.5 and ratios[int(0.9 * len(ratios))] <= 2.5, ratios
     # ... and no tensor by more than three times as much (two independent rounding-noise draws)
+    for r, name, e, eb in rows:
+        bound = max(2e-2, 3.0 * eb)
+        assert e <= bound, f"{name}: rel err {e:.3e} > {bound:.3e}"
+
+
+def _compare_fp32(loss_n, grads_n, loss_r, grads_r):
+    assert abs(loss_n - loss_r) <= 1e-4 * abs(loss_r), (loss_n, loss_r)
+    assert grads_n.keys() == grads_r.keys()
+    worst = ("", 0.0)
+    for name, gr in grads_r.items():
+        assert gr.abs().max().item() > 0, f"{name}: zero reference gradient"
+        e = rel_err(grads_n[name], gr)
+        worst = max(worst, (name, e), key=lambda t: t[1])
+        assert e <= 1e-3, f"{name}: rel err {e:.3e} > 1e-3"
+    print(f"  {len(grads_r)} gradients, worst {worst[0]} {worst[1]:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("sizes,b,T", [(SMALL, 2, 384), (CONFIG4_LAYER, *CONFIG4_BT)],
+                         ids=["small_two_layers_padded", "config4_one_layer"])
+def test_native_composition_fp32(sizes, b, T):
+    """Blocks on the native kernels end to end (front end, fused trapezoidal scan with D and the gated norm,
+    out_proj) against the reference composition with the oracle SSD, all fp32."""
+    model, tokens, targets = _model_and_batch(sizes, b, T, torch.float32, checkpoint=False)
+    set_native(model, True)
+    loss_n, grads_n = _step(model, tokens, targets, "native composition fp32")
+    set_native(model, False)
+    set_ssd(model, reference_ssd)
+    loss_r, grads_r = _step(model, tokens, targets, "reference composition, oracle fp32 SSD")
+    _compare_fp32(loss_n, grads_n, loss_r, grads_r)
+
+
+@pytest.mark.parametrize("sizes,b,T,checkpoint", [(SMALL, 2, 384, False), (CONFIG4_LAYER, *CONFIG4_BT, False),
+                                                   (CONFIG4, *CONFIG4_BT, True)],
+                         ids=["small_two_layers_padded", "config4_one_layer", "config4_24_layers"])
+def test_native_composition_bf16(sizes, b, T, checkpoint):
+    """The native composition in bf16 with the fused LM head, against the reference composition: its
+    gradients move from the fp32-SSD reference no more than the reference's own bf16 arithmetic moves them
+    (the criterion of test_training_step_bf16)."""
+    model, tokens, targets = _model_and_batch(sizes, b, T, torch.bfloat16, checkpoint)
+    set_native(model, True, head=True)
+    loss_n, grads_n = _step(model, tokens, targets, "native composition bf16")
+    set_native(model, False)
+    set_ssd(model, reference_ssd)
+    loss_r, grads_r = _step(model, tokens, targets, "reference composition, oracle fp32 SSD on bf16 values")
+    set_ssd(model, reference_ssd_bf16_storage)
+    loss_b, grads_b = _step(model, tokens, targets, "reference composition, oracle bf16 storage")
+    assert grads_n.keys() == grads_r.keys() == grads_b.keys()
+    rows = []
+    for name, gr in grads_r.items():
+        assert gr.abs().max().item() > 0, f"{name}: zero reference gradient"
+        e, eb = rel_err(grads_n[name], gr), rel_err(grads_b[name], gr)
+        rows.append((e / max(eb, 1e-12), name, e, eb))
+    rows.sort(reverse=True)
+    ratios = sorted(r[0] for r in rows)
+    print(f"  {len(rows)} gradients; native / reference-bf16 deviation: median {ratios[len(ratios) // 2]:.2f}, "
+          f"90th pct {ratios[int(0.9 * len(ratios))]:.2f}, max {ratios[-1]:.2f}", flush=True)
+    for r, name, e, eb in rows[:8]:
+        print(f"    {name:40s} native {e:.2e} reference-bf16 {eb:.2e} ratio {r:.2f}", flush=True)
+    assert abs(loss_n - loss_r) <= 1e-3 * abs(loss_r), (loss_n, loss_r)
+    assert ratios[len(ratios) // 2] <= 1.5 and ratios[int(0.9 * len(ratios))] <= 2.5, ratios
     for r, name, e, eb in rows:
         bound = max(2e-2, 3.0 * eb)
         assert e <= bound, f"{name}: rel err {e:.3e} > {bound:.3e}"
