@@ -23,7 +23,7 @@ struct Plan {
   int dtype, state_dtype;
   int64_t nslices, hslice, npass_blk, norm_blocks;
   // byte offsets inside each workspace
-  size_t o_chunks, o_seq0, o_cs, o_fast, o_hin, o_ypre, o_rstd, o_tzdt, o_tzrho, o_tzgam, o_tzcb, o_Dtok, o_hgam,
+  size_t o_chunks, o_seq0, o_cs, o_bfac, o_ffac, o_ffac2, o_fast, o_hin, o_ypre, o_rstd, o_tzdt, o_tzrho, o_tzgam, o_tzcb, o_Dtok, o_hgam,
       saved_bytes;
   size_t o_st, fwd_bytes;
   size_t o_dyp, o_dst, o_dtot, o_rowG, o_colG, o_eterm, o_dcs, o_xdx, o_dD, o_dA, o_dBp, o_dCp, o_dw, o_dS, o_dSf, o_dst16,
@@ -116,6 +116,7 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->o_chunks = take(MC * sizeof(ChunkInfo));
   p->o_seq0 = take((nseq + 1) * sizeof(int32_t));
   p->o_cs = take(MC * H * d.Qpad * sizeof(float));
+  p->o_bfac = take(MC * H * d.Qpad * sizeof(float));
   p->o_fast = take(MC * H * sizeof(int32_t));
   p->o_hin = take(MC * H * PN * es);
   p->o_ypre = d.has_z ? take((size_t)R * H * d.P * es) : 0;
@@ -130,6 +131,8 @@ int plan(const ssd_desc_t* s, Plan* p) {
   p->saved_bytes = off;
   off = 0;
   p->o_st = take(MC * H * PN * sizeof(float));
+  p->o_ffac = take(MC * H * d.Qpad * sizeof(float));
+  p->o_ffac2 = d.trapz == SSD_TRAPZ_DROP_BETA_DA ? take(MC * H * d.Qpad * sizeof(float)) : 0;
   p->fwd_bytes = off;
   off = 0;
   p->o_dyp = d.has_z ? take((size_t)R * H * d.P * es) : 0;
@@ -164,6 +167,7 @@ void bind_saved(const Plan& p, void* saved, SsdBufs* b) {
   b->chunks = reinterpret_cast<ChunkInfo*>(s + p.o_chunks);
   b->seq_chunk0 = reinterpret_cast<int32_t*>(s + p.o_seq0);
   b->cs = reinterpret_cast<float*>(s + p.o_cs);
+  b->bwd_fac = reinterpret_cast<float*>(s + p.o_bfac);
   b->fast = reinterpret_cast<int32_t*>(s + p.o_fast);
   b->hin = s + p.o_hin;
   b->ypre = p.d.has_z ? s + p.o_ypre : nullptr;
@@ -268,6 +272,8 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
   memset(&b, 0, sizeof(b));
   bind_saved(p, saved, &b);
   b.st = reinterpret_cast<float*>(scratch);
+  b.fwd_fac = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + p.o_ffac);
+  b.fwd_fac2 = p.o_ffac2 ? reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + p.o_ffac2) : nullptr;
   // trapezoidal mode: the scan's dt is gamma + rho, written by the coefficient kernel
   const float* dt = d.trapz ? b.tz_dt : a->dt;
   SsdIn in = {a->x, dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
@@ -284,7 +290,7 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
       SsdBufs bg = b;
       bg.hin = b.hgam;
       if (fused_state) {
-        SSD_TRY(launch_state_fwd_fused(d, bg, a->x, a->B, b.tz_gam, nullptr, nullptr, p.state_dtype, s));
+        SSD_TRY(launch_state_fwd_fused(d, bg, a->x, a->B, b.fwd_fac2, nullptr, nullptr, p.state_dtype, s));
       } else {
         SSD_TRY(launch_chunk_state(p.dtype, 0, d, bg, a->x, a->B, b.tz_gam, b.st, s));
         SSD_TRY(launch_state_pass_fwd(p.dtype, p.state_dtype, d, bg, nullptr, nullptr, s));
@@ -294,7 +300,7 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
   }
   if (fused_state) {
     SSD_PHASE(tm, SSD_PH_FWD_PASS,
-              launch_state_fwd_fused(d, b, a->x, a->B, dt, d.has_init ? a->init : nullptr,
+              launch_state_fwd_fused(d, b, a->x, a->B, b.fwd_fac, d.has_init ? a->init : nullptr,
                                      desc->want_final ? a->final_state : nullptr, p.state_dtype, s));
   } else {
     SSD_PHASE(tm, SSD_PH_FWD_STATE, launch_chunk_state(p.dtype, 0, d, b, a->x, a->B, dt, b.st, s));

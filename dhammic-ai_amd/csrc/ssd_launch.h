@@ -44,7 +44,7 @@ hipError_t launch_state_pass_bwd(int dtype, int state_dtype, const SsdDims& d, c
 // recurrence in one pass; the backward one writes b.dst16 and b.npass_blk partials
 bool state_fused_supported(int dtype, const SsdDims& d);
 int state_fused_slices(const SsdDims& d);
-hipError_t launch_state_fwd_fused(const SsdDims& d, const SsdBufs& b, const void* x, const void* B, const float* dt,
+hipError_t launch_state_fwd_fused(const SsdDims& d, const SsdBufs& b, const void* x, const void* B, const float* fac,
                                   const void* init, void* final_state, int state_dtype, hipStream_t s);
 hipError_t launch_state_bwd_fused(const SsdDims& d, const SsdBufs& b, const void* dy, const void* C,
                                   const void* dfinal, void* dinit, int state_dtype, hipStream_t s);

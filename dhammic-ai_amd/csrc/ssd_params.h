@@ -33,6 +33,12 @@ struct SsdBufs {
   void* ypre;              // [R][H][P] (T) y before the gated norm (has_z)
   float* rstd;             // [R] (has_z)
   float* st;               // fwd scratch: [max_chunks][H][Ppad][Npad] chunk-local states
+  // per-token factors of the fused state walks, [max_chunks][H][Qpad] (0 past a chunk's end):
+  // fwd_fac = exp(clamp(cs_last - cs_t)) dt_t (fwd scratch; fwd_fac2 with dt = gamma, the trapezoidal
+  // gamma walk); bwd_fac = exp(clamp(cs_t)) (saved)
+  float* fwd_fac;
+  float* fwd_fac2;
+  float* bwd_fac;
   // backward scratch
   void* dyp;               // [R][H][P] (T) gradient at y before the gated norm (has_z)
   float* dst;              // [max_chunks][H][Ppad][Npad] local dh, then gradient leaving each chunk

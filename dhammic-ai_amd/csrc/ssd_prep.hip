@@ -70,13 +70,18 @@ hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t*
 // In-chunk inclusive cumsum of a (ssd_scan.py:364-368), one wave per
 // (chunk, head), fp32. Positions past the chunk's length carry a = 0, so
 // cs[Qpad-1] is the chunk total. Optionally writes the reference's
-// A_cumsum (b, h, c, Q) in the input dtype.
+// A_cumsum (b, h, c, Q) in the input dtype, and the fused state walks'
+// per-token factors (0 past the chunk's length): bfac = exp(clamp(cs_t)),
+// ffac = exp(clamp(cs_last - cs_t)) dt_t (trapezoidal mode: zeros here, the
+// coefficient kernel writes the chunk's positions with its own dt), ffac2
+// (trapezoidal gamma walk: zeros here likewise).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                       const void* __restrict__ Av, const float* __restrict__ dt,
                                                       float* __restrict__ cs, T* __restrict__ acs_out,
-                                                      int32_t* __restrict__ fast) {
+                                                      int32_t* __restrict__ fast, float* __restrict__ ffac,
+                                                      float* __restrict__ ffac2, float* __restrict__ bfac) {
   const int c = blockIdx.x;
   const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
@@ -84,11 +89,12 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
   const ChunkInfo ci = chunks[c];
   if (ci.len == 0) return;
   const int per = d.Qpad / 64;  // 1, 2 or 4 consecutive positions per lane
-  float v[4];
+  float v[4], dtv[4];
   float run = 0.0f;
   for (int e = 0; e < per; ++e) {
     const int l = lane * per + e;
     float a = 0.0f;
+    dtv[e] = (d.has_dt && !d.trapz && l < ci.len) ? dt[(ci.row0 + l) * d.H + h] : 1.0f;
     if (d.a_mode == 2) {
       // the caller's inclusive cumsum: differences are not needed, keep it as is
       const int nch = d.seqlen / d.Q;
@@ -101,7 +107,7 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
       const int64_t row = ci.row0 + l;
       if (d.a_mode == 0) {
         const float* A = reinterpret_cast<const float*>(Av);
-        a = (d.has_dt ? dt[row * d.H + h] : 1.0f) * A[h];
+        a = dtv[e] * A[h];
       } else {
         const T* A = reinterpret_cast<const T*>(Av);
         a = to_f(A[row * d.H + h]);
@@ -122,6 +128,17 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
   }
   float* out = cs + ((int64_t)c * d.H + h) * d.Qpad;
   for (int e = 0; e < per; ++e) out[lane * per + e] = v[e];
+  if (ffac) {
+    const int64_t o = ((int64_t)c * d.H + h) * d.Qpad;
+    const float tot = __shfl(v[per - 1], 63, 64);  // cs[Qpad - 1], the chunk total
+    for (int e = 0; e < per; ++e) {
+      const int l = lane * per + e;
+      const bool in = l < ci.len;
+      ffac[o + l] = (in && !d.trapz) ? exp_clamp(tot - v[e]) * dtv[e] : 0.0f;
+      if (ffac2) ffac2[o + l] = 0.0f;
+      bfac[o + l] = in ? exp_clamp(v[e]) : 0.0f;
+    }
+  }
   if (fast) {
     // Factorised-decay guard: cs non-increasing over the chunk (every a <= 0)
     // and each 64-token block's drop cs[64 j] - cs[64 j + 63] at most
@@ -161,10 +178,10 @@ hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, co
   dim3 grid(d.max_chunks, (d.H + 3) / 4);
   if (dtype == 1)
     hipLaunchKernelGGL(k_chunk_cumsum<bf16>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
-                       reinterpret_cast<bf16*>(A_cumsum_out), b.fast);
+                       reinterpret_cast<bf16*>(A_cumsum_out), b.fast, b.fwd_fac, b.fwd_fac2, b.bwd_fac);
   else
     hipLaunchKernelGGL(k_chunk_cumsum<float>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
-                       reinterpret_cast<float*>(A_cumsum_out), b.fast);
+                       reinterpret_cast<float*>(A_cumsum_out), b.fast, b.fwd_fac, b.fwd_fac2, b.bwd_fac);
   return hipGetLastError();
 }
 

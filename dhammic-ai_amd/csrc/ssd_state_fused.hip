@@ -19,7 +19,8 @@
 // 32 x 32 tile (p tile w % PT, n tile w / PT). Blocks of one (head, sequence) are numbered
 // onto one XCD (same block index mod 8) so their shared x / dy rows come from
 // HBM once. Tokens go 64 at a time through a ring of three LDS slots filled by
-// buffer_load ... lds (x or dy rows, the pair's B or C columns, cs and dt),
+// buffer_load ... lds (x or dy rows, the pair's B or C columns, and the tokens'
+// precomputed factors exp(clamp(cs_last - cs_t)) dt_t or exp(clamp(cs_t))),
 // issued two steps ahead with explicit vmcnt waits, so no register holds
 // staged data and every step's wait counts exactly. Both MFMA operands are
 // read with ds_read_b64_tr_b16 from granule-permuted rows (the contraction is
@@ -38,7 +39,7 @@ struct StateCfg {
   static constexpr int R = 3;                   // ring slots
   static constexpr int UB = 64 * PP * 2;        // x / dy rows of a step
   static constexpr int VB = 64 * 64 * 2;        // B / C rows of a step, the pair's 64 columns
-  static constexpr int SLOT = UB + VB + NW * 256;  // + one 64-float row per wave (cs, dt, spare)
+  static constexpr int SLOT = UB + VB + NW * 256;  // + one 64-float row per wave (wave 0: the factors)
   static constexpr int UI = UB / 1024, VI = VB / 1024;  // 1 KB DMA instructions
   static constexpr int PERW = (UI + VI) / NW;   // row DMAs per wave and step
   static constexpr int D = PERW + 1;            // DMAs per wave and step (+ one scalar row)
@@ -49,7 +50,7 @@ struct StateCfg {
   static constexpr int TW = 24;                 // s_tile row pitch (elements), 64 x 16 tiles
   static constexpr int TWE = PT == 2 ? 64 * TW : 32 * TP;  // s_tile elements per wave
   static size_t bytes(bool bwd) {
-    return (size_t)R * SLOT + NW * 64 * 4 + NW * TWE * 2 + (bwd ? NW * 2048 : 0) + 64;
+    return (size_t)R * SLOT + NW * TWE * 2 + (bwd ? NW * 2048 : 0) + 64;
   }
 };
 
@@ -77,7 +78,7 @@ struct StateCtx {
   SsdDims d;
   const ChunkInfo* chunks;
   const float* cs;
-  const float* dt;
+  const float* fac;  // per-token factors [max_chunks][H][Qpad] (0 past a chunk's end)
   const bf16* U;
   const bf16* V;
   bf16* hst;
@@ -123,9 +124,7 @@ struct IssueLanes {
   static_assert(Cfg::UI % Cfg::NW == 0 && Cfg::VI % Cfg::NW == 0, "per-wave DMA split");
   int ou[UPW], ov[VPW];  // lane's byte offset within the step's rows (SSD_BUF_SIZE: column outside)
   int lu[UPW], lv[VPW];  // lane's row within the step
-  int os;                // scalar row: lane's byte offset (SSD_BUF_SIZE: this wave loads none)
-  int sstr;              // scalar row: bytes per token
-  bool sdt;              // the scalar row is dt (masked past the step's rows)
+  int os;                // factor row: lane's byte offset (SSD_BUF_SIZE: this wave loads none)
 };
 
 template <int PT, bool FWD>
@@ -149,9 +148,7 @@ __device__ __forceinline__ IssueLanes<PT> issue_lanes(const StateCtx& x, int lan
     il.lv[q] = r;
     il.ov[q] = 64 * x.np + gcol < d.N ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE;
   }
-  il.sdt = FWD && d.has_dt && x.w == 1;
-  il.sstr = il.sdt ? d.H * 4 : 4;
-  il.os = x.w == 0 ? lane * 4 : (il.sdt ? lane * d.H * 4 : SSD_BUF_SIZE);
+  il.os = x.w == 0 ? lane * 4 : SSD_BUF_SIZE;
   return il;
 }
 
@@ -164,7 +161,7 @@ __device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<
   u.ci = x.chunks[c];
   u.bu = x.U + (int64_t)u.ci.row0 * x.urow + x.ucol;
   u.bv = x.V + (int64_t)u.ci.row0 * x.vrow + x.vcol;
-  u.bs = il.sdt ? x.dt + (int64_t)u.ci.row0 * d.H + x.h : x.cs + ((int64_t)c * d.H + x.h) * d.Qpad;
+  u.bs = x.fac + ((int64_t)c * d.H + x.h) * d.Qpad;
 }
 
 // One step's DMAs into ring slot `nxt`: StateCfg::D per wave, also past the last step
@@ -195,7 +192,7 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
         rv, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + (x.w * IL::VPW + q) * 1024), 16, vo, sv, 0, 0);
   }
   {
-    const int vo = (!il.sdt || lane < nrows) ? il.os : SSD_BUF_SIZE, so = t0i * il.sstr;
+    const int vo = il.os, so = t0i * 4;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB + x.w * 256), 4, vo, so, 0, 0);
   }
@@ -215,7 +212,7 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
 // own for them, and the slot waits stay the explicit ones of the caller.
 template <int PT, bool FWD>
 __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
-                                           unsigned char* __restrict__ nxt, float* __restrict__ cw,
+                                           unsigned char* __restrict__ nxt,
                                            bf16* __restrict__ tw, bf16* __restrict__ hbw, float* __restrict__ red,
                                            const IssueLanes<PT>& il, IssueCur& ui, Cursor& uc, float& tot, int& st,
                                            int& s_start, floatx16& acc, floatx16& run) {
@@ -263,20 +260,15 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   }
   const bf16* tu = reinterpret_cast<const bf16*>(cur);
   const bf16* tv = reinterpret_cast<const bf16*>(cur + Cfg::UB);
-  const float* scal = reinterpret_cast<const float*>(cur + Cfg::UB + Cfg::VB);
-  // per-token factor of the step's B / C rows (lane = token), for this wave's own use
-  {
-    const float cst = scal[lane];
-    const float dtt = (FWD && d.has_dt) ? scal[64 + lane] : 1.0f;
-    const float f = FWD ? exp_clamp(tot - cst) * dtt : exp_clamp(cst);
-    cw[lane] = t0 + lane < clen ? f : 0.0f;
-  }
+  // the step's per-token factors of the B / C rows (precomputed, 0 past the chunk's end): read
+  // straight from the slot, eight consecutive tokens per lane
+  const float* fac = reinterpret_cast<const float*>(cur + Cfg::UB + Cfg::VB);
   if constexpr (WIDE) {
     // 64 p x 16 n: the scaled B / C operand is shared by the four p blocks
 #pragma unroll
     for (int kk = 0; kk < 64; kk += 32) {
-      const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 4));
-      const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 4) + 4);
+      const floatx4 f0 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 4));
+      const floatx4 f1 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 4) + 4);
       bf16x8 b = swz_tr8_16<64>(tv, kk, 16 * x.w, lane);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -291,8 +283,8 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   } else {
 #pragma unroll
     for (int kk = 0; kk < 64; kk += 16) {
-      const floatx4 f0 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5));
-      const floatx4 f1 = *reinterpret_cast<const floatx4*>(cw + kk + 8 * (lane >> 5) + 4);
+      const floatx4 f0 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 5));
+      const floatx4 f1 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 5) + 4);
       bf16x8 b = swz_tr8<64>(tv, kk, 32 * x.ntl, lane);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -348,7 +340,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
 template <int PT, bool FWD>
 __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2, 2))) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
-                                                         const float* __restrict__ cs, const float* __restrict__ dt,
+                                                         const float* __restrict__ cs, const float* __restrict__ fac,
                                                          const bf16* __restrict__ U, const bf16* __restrict__ V,
                                                          bf16* __restrict__ hst, const bf16* __restrict__ hin_in,
                                                          const void* __restrict__ s_in, void* __restrict__ s_out,
@@ -357,8 +349,7 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   constexpr int TP = Cfg::TP, SLOT = Cfg::SLOT;
   constexpr bool WIDE = state_wide<PT, FWD>();
   extern __shared__ __align__(16) unsigned char smem[];
-  float* cw = reinterpret_cast<float*>(smem + Cfg::R * SLOT);             // [NW][64] per-token factors
-  bf16* s_tile = reinterpret_cast<bf16*>(cw + Cfg::NW * 64);              // [NW][TWE] state tiles
+  bf16* s_tile = reinterpret_cast<bf16*>(smem + Cfg::R * SLOT);          // [NW][TWE] state tiles
   bf16* hb = s_tile + Cfg::NW * Cfg::TWE;                                 // [NW][1024] (backward: h_in)
   float* red = reinterpret_cast<float*>(hb + (FWD ? 0 : Cfg::NW * 1024)); // [NW]
 
@@ -388,7 +379,7 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   x.nt_ok = x.nt < x.NTn;
   x.chunks = chunks;
   x.cs = cs;
-  x.dt = dt;
+  x.fac = fac;
   x.U = U;
   x.V = V;
   x.hst = hst;
@@ -440,7 +431,7 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
     wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
     lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
-    state_step<PT, FWD>(x, cur, nxt, cw + x.w * 64, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, il, ui, uc, tot, st,
+    state_step<PT, FWD>(x, cur, nxt, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, il, ui, uc, tot, st,
                         s_start, acc, run);
   };
   while (uc.k < x.nch) {
@@ -472,7 +463,7 @@ bool state_fused_supported(int dtype, const SsdDims& d) {
 int state_fused_slices(const SsdDims& d) { return d.Npad / 32; }
 
 template <int PT, bool FWD>
-static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* dt,
+static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* fac,
                                bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
                                hipStream_t s) {
   const int units = d.H * d.nseq, npr = (d.Npad / 32 + 1) / 2;
@@ -480,30 +471,30 @@ static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u
   const size_t lds = StateCfg<PT>::bytes(!FWD);
   ensure_lds(k_state_fused<PT, FWD>, lds);
   hipLaunchKernelGGL((k_state_fused<PT, FWD>), grid, dim3(StateCfg<PT>::NTHR), lds, s, d, b.chunks, b.seq_chunk0,
-                     b.cs, dt, u, v, hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
+                     b.cs, fac, u, v, hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
 }
 
 template <bool FWD>
-static hipError_t state_fused_t(const SsdDims& d, const SsdBufs& b, const void* U, const void* V, const float* dt,
+static hipError_t state_fused_t(const SsdDims& d, const SsdBufs& b, const void* U, const void* V, const float* fac,
                                 bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
                                 hipStream_t s) {
   const bf16* u = reinterpret_cast<const bf16*>(U);
   const bf16* v = reinterpret_cast<const bf16*>(V);
   switch (d.Ppad / 32) {
-    case 1: state_fused_launch<1, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s); break;
-    case 2: state_fused_launch<2, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s); break;
-    default: state_fused_launch<4, FWD>(d, b, u, v, dt, hst, hin_in, s_in, s_out, state_bf16, s);
+    case 1: state_fused_launch<1, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    case 2: state_fused_launch<2, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    default: state_fused_launch<4, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s);
   }
   return hipGetLastError();
 }
-hipError_t launch_state_fwd_fused(const SsdDims& d, const SsdBufs& b, const void* x, const void* B, const float* dt,
+hipError_t launch_state_fwd_fused(const SsdDims& d, const SsdBufs& b, const void* x, const void* B, const float* fac,
                                   const void* init, void* final_state, int state_dtype, hipStream_t s) {
-  return state_fused_t<true>(d, b, x, B, dt, reinterpret_cast<bf16*>(b.hin), nullptr, init, final_state,
+  return state_fused_t<true>(d, b, x, B, fac, reinterpret_cast<bf16*>(b.hin), nullptr, init, final_state,
                              state_dtype == 1, s);
 }
 
 hipError_t launch_state_bwd_fused(const SsdDims& d, const SsdBufs& b, const void* dy, const void* C,
                                   const void* dfinal, void* dinit, int state_dtype, hipStream_t s) {
-  return state_fused_t<false>(d, b, dy, C, nullptr, b.dst16, reinterpret_cast<const bf16*>(b.hin), dfinal, dinit,
+  return state_fused_t<false>(d, b, dy, C, b.bwd_fac, b.dst16, reinterpret_cast<const bf16*>(b.hin), dfinal, dinit,
                               state_dtype == 1, s);
 }

@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(256) k_trapz_coef(SsdDims d, const int32_t* __
   const int64_t row = id / d.H;
   const int h = (int)(id - row * d.H);
   int64_t start, end;
-  tz_seq(d, cu, row, start, end);
+  const int seq = tz_seq(d, cu, row, start, end);
   float rho = 0.0f;
   if (row + 1 < end) rho = to_f(beta[id + d.H]) * exp2_fast(-to_f(A[id + d.H]) * SSD_LOG2E);
   const float gm = to_f(gamma[id]);
@@ -90,6 +90,16 @@ __global__ void __launch_bounds__(256) k_trapz_coef(SsdDims d, const int32_t* __
   b.tz_gam[id] = gm;
   b.tz_dt[id] = gm + rho;
   b.Dtok[id] = (d.has_D ? D[h] : 0.0f) + gm * b.tz_cb[row * d.G + h / d.hpg];
+  // the fused state walks' per-token factors exp(clamp(cs_last - cs_t)) dt_t, with dt = gamma + rho
+  // (and dt = gamma for the gamma path's walk); positions past a chunk's end keep the cumsum's zeros
+  if (b.fwd_fac && row < end) {
+    const int64_t pos = tz_pos(d, b, row, start, seq) + (int64_t)h * d.Qpad;
+    const int64_t t = (row - start) % d.Q;
+    const float cst = b.cs[pos], tot = b.cs[pos - t + d.Qpad - 1];
+    const float e = exp_clamp(tot - cst);
+    b.fwd_fac[pos] = e * (gm + rho);
+    if (b.fwd_fac2) b.fwd_fac2[pos] = e * gm;
+  }
 }
 
 // Column / row path only (the fused path does this inside k_bwd_fact and k_bwd_gemm): per (row, group)
