@@ -222,7 +222,15 @@ class _LazyCache(dict):
     def __init__(self, a, A_cumsum, chunk):
         super().__init__(L=None, decay_chunk=None, A_cumsum=A_cumsum)
         self._a = a
+        self._a_version = a._version
         self._chunk = chunk
+
+    def built_from(self, A):
+        """Whether this cache is the one a call on this very A (same storage, unmodified since)
+        returned: its A_cumsum is then the in-kernel fp32 cumsum of A, stored in A's dtype."""
+        a = self._a
+        return (A.data_ptr() == a.data_ptr() and A.shape == a.shape and A.stride() == a.stride()
+                and A.dtype == a.dtype and A.device == a.device and A._version == self._a_version)
 
     def _fill(self, key):
         v = dict.__getitem__(self, key)
@@ -297,14 +305,18 @@ class _CachePlan:
     A_used: bool               # A enters the computation (else its gradient is None, as in :533)
 
 
-def _cache_plan(x, A, chunk, has_L, has_dc, acs):
+def _cache_plan(x, A, chunk, has_L, has_dc, acs, recompute=False):
     """Which decays come from a cache (ssd_scan.py:364-406): the intra-chunk L, the inter-chunk
     decay_chunk, A_cumsum (state build, Y_off, and decay_chunk when not cached itself). A cached
     tensor takes no gradient, so each one drops its terms from dA; A takes none at all when it feeds
     nothing (L and A_cumsum both cached). The kernels compute every decay from A_cumsum (the cached
     one, or the cumsum of A): a cached L or decay_chunk is taken to be the one a call on the same
     decays returned, which is how the reference's caller builds its cache
-    (mamba_base_engine.py:170-181)."""
+    (mamba_base_engine.py:170-181). ``recompute``: the cache came from this module's call on this
+    same A, so the kernels rebuild that call's fp32 cumsum from A rather than read its stored copy.
+    In bf16 the stored copy is rounded, and differences of rounded cumsums lose the intra-chunk
+    decays of nearby tokens, which the reference takes from segsum(A) or its cached L (:104-116).
+    The dropped gradient terms are the cache's all the same."""
     b, T, H = x.shape[:3]
     nch = T // chunk
     if acs is not None:
@@ -312,11 +324,11 @@ def _cache_plan(x, A, chunk, has_L, has_dc, acs):
     skip = ((C_.SSD_DA_SKIP_INTRA if has_L else 0)
             | (C_.SSD_DA_SKIP_CUMSUM | C_.SSD_DA_SKIP_CHUNK if acs is not None else 0)
             | (C_.SSD_DA_SKIP_CHUNK if has_dc else 0))
-    a_mode = C_.SSD_A_CUMSUM if acs is not None else C_.SSD_A_PER_TOKEN
+    from_acs = acs is not None and not recompute
+    a_mode = C_.SSD_A_CUMSUM if from_acs else C_.SSD_A_PER_TOKEN
     cfg = _Cfg(chunk=chunk, a_mode=a_mode, nseq=b, varlen=False, state_code=_code(x.dtype, "x"),
                want_acs=acs is None, eps=0.0, dA_skip=skip)
-    return _CachePlan(cfg, None if acs is None else acs.detach().contiguous(),
-                      not (has_L and acs is not None))
+    return _CachePlan(cfg, acs.detach().contiguous() if from_acs else None, not (has_L and acs is not None))
 
 
 def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
@@ -343,10 +355,12 @@ def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
     N = B.shape[-1]
     init = None if initial_states is None else initial_states.reshape(b, H, P, N).contiguous()
     L_in = dc_in = acs_in = None
+    recompute = False
     if isinstance(cache, _LazyCache):
         # every key is present (L and decay_chunk lazily, from the same decays)
         has_L = has_dc = True
         acs_in = cache.cumsum_tensor()
+        recompute = cache.built_from(A)
     elif cache is not None:
         L_in, dc_in, acs_in = cache.get("L"), cache.get("decay_chunk"), cache.get("A_cumsum")
         has_L, has_dc = L_in is not None, dc_in is not None
@@ -357,7 +371,7 @@ def fused_ssd_scan(x, A, B, C, chunk_size, initial_states=None, cache=None):
             _check_cached("decay_chunk", dc_in, (b, H, nch + 1, nch + 1), x)
     else:
         has_L = has_dc = False
-    plan = _cache_plan(x, A, chunk, has_L, has_dc, acs_in)
+    plan = _cache_plan(x, A, chunk, has_L, has_dc, acs_in, recompute)
     a = A.contiguous()
     Y, final, acs = _SsdFunction.apply(plan.cfg, x.contiguous(), None, a if plan.A_used else a.detach(),
                                        B.contiguous(), C.contiguous(), None, None, None, init, None, plan.acs)
