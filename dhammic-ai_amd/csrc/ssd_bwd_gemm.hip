@@ -76,59 +76,60 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const int MC = d.max_chunks, Qpad = d.Qpad;
   const int h0 = g * d.hpg, h1 = h0 + d.hpg;
 
-  // ---- one head's inputs into ring slot `slot` (kPerWave DMA instructions per wave) ----
-  auto issue = [&](int h, unsigned char* base) {
-    const __amdgpu_buffer_rsrc_t rh = buf_rsrc(hin + ((int64_t)c * d.H + h) * Cfg::HIN);
-    const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dst + ((int64_t)c * d.H + h) * Cfg::HIN);
-    const int64_t xoff = (int64_t)(ci.row0 + 64 * kb) * xrow + (int64_t)h * d.P;
-    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + xoff);
-    const __amdgpu_buffer_rsrc_t ry = buf_rsrc(dy + xoff);
-    // h_in and dst: rows p of NP elements, 512 / NP rows per instruction
-    constexpr int TG = NP / 8, TRI = 64 / TG;
+  // ---- one head's inputs into a ring slot (kPerWave DMA instructions per issuing wave) ----
+  // Waves 0-1 load h_in and the x rows, waves 2-3 dst and the dy rows, each its own fixed share, and
+  // one scalar row each (wave 0 cs of the block's tokens, wave 1 dt, wave 2 cs of the chunk's last
+  // position, wave 3 gamma in trapezoidal mode). Every per-lane offset and every base is fixed for
+  // the block; a head only moves the bases by a wave-uniform soffset.
+  constexpr int TPW = Cfg::kTileDma / 2, RPW = Cfg::kRowDma / 2;  // tile / row DMAs per issuing wave
+  constexpr int TG = NP / 8, TRI = 64 / TG;  // h_in / dst rows of NP elements: granules per row, rows per DMA
+  constexpr int XG = PP / 8, XRI = 64 / XG;  // x / dy rows of PP elements
+  const bool second = w >= 2;
+  int vt[TPW], vr[RPW];
 #pragma unroll
-    for (int q = 0; q < Cfg::kTileDma * 2 / 4; ++q) {
-      const int qq = w * (Cfg::kTileDma * 2 / 4) + q;  // 0 .. 2 kTileDma - 1
-      const bool second = qq >= Cfg::kTileDma;
-      const int qi = second ? qq - Cfg::kTileDma : qq;
-      const int r = qi * TRI + lane / TG, j = lane % TG;
-      const int off = (r * NP + (swz_tr<NP>(r, j) << 3)) * 2;
+  for (int q = 0; q < TPW; ++q) {
+    const int qi = (w & 1) * TPW + q, r = qi * TRI + lane / TG;
+    vt[q] = (r * NP + (swz_tr<NP>(r, lane % TG) << 3)) * 2;
+  }
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int qi = (w & 1) * RPW + q, r = qi * XRI + lane / XG;
+    const int gcol = swz_nat<PP>(r, lane % XG) << 3;
+    vr[q] = (r < nrows && gcol < d.P) ? (int)((r * xrow + gcol) * 2) : SSD_BUF_SIZE;
+  }
+  const int64_t row_b = (int64_t)(ci.row0 + 64 * kb);
+  const bf16* tile_base = (second ? dst : hin) + (int64_t)c * d.H * Cfg::HIN;
+  const bf16* rows_base = (second ? dy : x) + row_b * xrow;
+  const bool s_tok = (w == 1 && d.has_dt) || (w == 3 && d.trapz);  // a per-token [R][H] row
+  const float* scal_base = w == 1 && d.has_dt ? dt + row_b * d.H
+                         : w == 3 && d.trapz ? tz_gam + row_b * d.H : cs + (int64_t)c * d.H * Qpad;
+  const int s_vo = s_tok ? (lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE)
+                 : w == 0 ? (64 * kb + lane) * 4 : w == 1 ? SSD_BUF_SIZE : (Qpad - 1) * 4;
+  const int s_str = s_tok ? 4 : Qpad * 4;  // soffset bytes per head
+  auto issue = [&](int h, unsigned char* base) {
+    const __amdgpu_buffer_rsrc_t rt = buf_rsrc(tile_base), rr = buf_rsrc(rows_base), rs = buf_rsrc(scal_base);
+    const int so_t = h * Cfg::HIN * 2, so_r = h * d.P * 2;
+    unsigned char* bt = base + (second ? Cfg::HIN * 2 : 0);
+    unsigned char* br = base + (2 * Cfg::HIN + (second ? Cfg::XT : 0)) * 2;
+    // (each offset goes through a plain int, so that the target builtins' calls stay non-dependent)
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) {
+      const int vo = vt[q];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(bt + ((w & 1) * TPW + q) * 1024),
+                                               16, vo, so_t, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int vo = vr[q];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(br + ((w & 1) * RPW + q) * 1024),
+                                               16, vo, so_r, 0, 0);
+    }
+    {
+      const int vo = s_vo, so = h * s_str;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          second ? rd : rh,
-          (__attribute__((address_space(3))) void*)(base + (second ? Cfg::HIN * 2 : 0) + qi * 1024), 16, off, 0, 0,
+          rs, (__attribute__((address_space(3))) void*)(base + (2 * Cfg::HIN + 2 * Cfg::XT) * 2 + w * 256), 4, vo, so, 0,
           0);
     }
-    // x and dy rows of the block: PP elements per row, 512 / PP rows per instruction
-    constexpr int XG = PP / 8, XRI = 64 / XG;
-#pragma unroll
-    for (int q = 0; q < Cfg::kRowDma * 2 / 4; ++q) {
-      const int qq = w * (Cfg::kRowDma * 2 / 4) + q;
-      const bool second = qq >= Cfg::kRowDma;
-      const int qi = second ? qq - Cfg::kRowDma : qq;
-      const int r = qi * XRI + lane / XG, j = lane % XG;
-      const int gcol = swz_nat<PP>(r, j) << 3;
-      const bool ok = r < nrows && gcol < d.P;
-      const int off = ok ? (int)((r * xrow + gcol) * 2) : SSD_BUF_SIZE;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          second ? ry : rx,
-          (__attribute__((address_space(3))) void*)(base + (2 * Cfg::HIN + (second ? Cfg::XT : 0)) * 2 + qi * 1024),
-          16, off, 0, 0, 0);
-    }
-    // cs of the block's tokens, dt, cs of the chunk's last position (4 bytes per lane)
-    unsigned char* sc = base + (2 * Cfg::HIN + 2 * Cfg::XT) * 2 + w * 256;
-    const float* csh = cs + ((int64_t)c * d.H + h) * Qpad;
-    int off;
-    __amdgpu_buffer_rsrc_t rs;
-    if (w == 1) {
-      rs = buf_rsrc(dt + (int64_t)(ci.row0 + 64 * kb) * d.H + h);
-      off = lane < nrows && d.has_dt ? lane * d.H * 4 : SSD_BUF_SIZE;
-    } else if (w == 3 && d.trapz) {  // trapezoidal mode: gamma of the block's tokens
-      rs = buf_rsrc(tz_gam + (int64_t)(ci.row0 + 64 * kb) * d.H + h);
-      off = lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE;
-    } else {
-      rs = buf_rsrc(csh);
-      off = w == 0 ? (64 * kb + lane) * 4 : (Qpad - 1) * 4;
-    }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)sc, 4, off, 0, 0, 0);
   };
 
   // trapezoidal mode: sum_h gamma (x_t . dy_t), the diagonal of dS (dC waves)
@@ -162,7 +163,9 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
     issue(head(0), smem);
     if (1 < nhd) issue(head(1), smem + Cfg::kSlot);
   }
-  for (int k = 0; k < nhd; ++k) {
+  // head k reads slot k % 3 and refills slot (k + 2) % 3; the loop below is unrolled over the three
+  // slots, so every slot address is a constant
+  auto head_step = [&](int k, const unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
     const int h = head(k);
     // this wave's loads of head k are done (those of k + 1 may still fly); then every wave's
     if (!brole) {
@@ -170,7 +173,7 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       else wait_vm<0>();
     }
     lds_barrier();  // head k visible in LDS; slot (k + 2) % 3 is free (head k - 1 done)
-    ring_step(smem + (k % 3) * Cfg::kSlot, smem + ((k + 2) % 3) * Cfg::kSlot, !brole && k + 2 < nhd,
+    ring_step(cur, nxt, !brole && k + 2 < nhd,
               [&](unsigned char* nxt) { issue(head(k + 2), nxt); }, [&](const unsigned char* base) {
     if (brole && d.da_only) return;  // decay gradient only: no dB
     lane = opaque_lane();
@@ -229,6 +232,11 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
       }
     }
     });
+  };
+  for (int k = 0; k < nhd; k += 3) {
+    head_step(k, smem, smem + 2 * Cfg::kSlot);
+    if (k + 1 < nhd) head_step(k + 1, smem + Cfg::kSlot, smem);
+    if (k + 2 < nhd) head_step(k + 2, smem + 2 * Cfg::kSlot, smem + Cfg::kSlot);
   }
 
   if (d.da_only) return;  // decay gradient only: the Y_off term above is all it needs
