@@ -100,7 +100,9 @@ int plan(const ssd_desc_t* s, Plan* p) {
   } else {
     p->nrowg = 1;
     const int64_t per_slice = max_chunks * d.G * (d.Qpad / SSD_BLK);
-    ns = (2048 + per_slice - 1) / per_slice;
+    // at least ~1024 column blocks (32 heads per slice at config 2: fewer dS partials than 16, and the
+    // block's S and B set-up spread over more heads)
+    ns = (1024 + per_slice - 1) / per_slice;
   }
   if (ns < 1) ns = 1;
   if (ns > d.hpg) ns = d.hpg;
