@@ -116,11 +116,12 @@ def phase_models(nchunks):
     st16 = nchunks * H * P * N * es          # hin or dst (bf16, one state per chunk and head)
     nseq = len(varlen_lengths()) if CFG_ID == 3 else b
     fin = nseq * H * P * N * 4               # final state / dfinal / dinit (fp32)
-    cs = nchunks * H * Q * 4                 # in-chunk cumsum, and each per-token fp32 vector
+    cs = nchunks * H * Q * 4                 # in-chunk cumsum, and each per-token fp32 vector (the walks' factors)
     dS = nchunks * G * (nb * (nb + 1) // 2) * 64 * 64 * 4   # head-summed dS tiles (fp32)
     m = {
-        "cumsum": (0, dt + cs),
-        "fwd_pass": (R * H * 2 * N * P, x + bc + dt + cs + st16 + fin),
+        # the cumsum also writes the state walks' per-token factors (forward and backward)
+        "cumsum": (0, dt + 3 * cs),
+        "fwd_pass": (R * H * 2 * N * P, x + bc + cs + st16 + fin),
         "fwd_scan": (R * (G * (Q + 1) * N + H * ((Q + 1) * P + 2 * N * P)), 2 * x + 2 * bc + dt + cs + st16),
         "norm_fwd": (0, 3 * x + R * 4),
         "norm_bwd": (0, 5 * x + R * 4),
