@@ -414,7 +414,7 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
     b.dst16 = nullptr;     // and read dst in fp32
   }
   const bool fused_state = fused && state_fused_supported(p.dtype, d);
-  if (fused_state) b.npass_blk = state_fused_slices(d);  // dtot partials: one per headdim slice
+  if (fused_state) b.npass_blk = state_fused_slices(d);  // dtot partials: one per 32 x 32 state tile
   const void* dY = a->dy;
   if (d.has_z) {
     SSD_PHASE(tm, SSD_PH_NORM_BWD, launch_gated_norm_bwd(p.dtype, d, b, in, a->dy, a->dz, s));

@@ -50,7 +50,7 @@ struct StateCfg {
   static constexpr int TW = 24;                 // s_tile row pitch (elements), 64 x 16 tiles
   static constexpr int TWE = PT == 2 ? 64 * TW : 32 * TP;  // s_tile elements per wave
   static size_t bytes(bool bwd) {
-    return (size_t)R * SLOT + NW * TWE * 2 + (bwd ? NW * 2048 : 0) + 64;
+    return (size_t)R * SLOT + NW * TWE * 2 + (bwd ? NW * 2048 : 0);
   }
 };
 
@@ -90,25 +90,52 @@ struct StateCtx {
   bool nt_ok;
 };
 
-// A walk position: chunk index k of the sequence, token offset t in it, and the
-// chunk's table entry (fetched when the position enters the chunk, a step before use).
+// Chunk-table index of walk position k (clamped to the sequence's last chunk).
+template <bool FWD>
+__device__ __forceinline__ int walk_chunk(const StateCtx& x, int k) {
+  const int kc = min(k, x.nch - 1);
+  return __builtin_amdgcn_readfirstlane(FWD ? x.c0 + kc : x.c1 - 1 - kc);
+}
+// Total log-decay (cs at the last padded position) of chunk c for the walk's head.
+__device__ __forceinline__ float chunk_total(const StateCtx& x, int c) {
+  return x.cs[((int64_t)c * x.d.H + x.h) * x.d.Qpad + x.d.Qpad - 1];
+}
+
+// A walk position: chunk index k of the sequence, token offset t in it, the chunk's table
+// entry and total log-decay, and those of the next chunk, loaded a whole chunk before use so
+// that entering a chunk waits on no scalar load.
 struct Cursor {
   int k, t, c;
-  ChunkInfo ci;
+  ChunkInfo ci, nci;
+  float tot, ntot;
 };
 
 template <bool FWD>
-__device__ __forceinline__ void cursor_fetch(const StateCtx& x, Cursor& u) {
-  const int kc = min(u.k, x.nch - 1);
-  u.c = __builtin_amdgcn_readfirstlane(FWD ? x.c0 + kc : x.c1 - 1 - kc);
+__device__ __forceinline__ void cursor_init(const StateCtx& x, Cursor& u) {
+  u.c = walk_chunk<FWD>(x, 0);
   u.ci = x.chunks[u.c];
+  u.tot = chunk_total(x, u.c);
+  const int cn = walk_chunk<FWD>(x, 1);
+  u.nci = x.chunks[cn];
+  u.ntot = chunk_total(x, cn);
+}
+// Enter chunk u.k (the one after the current) and load the entry and total of the chunk after it.
+template <bool FWD>
+__device__ __forceinline__ void cursor_next(const StateCtx& x, Cursor& u) {
+  u.c = walk_chunk<FWD>(x, u.k);
+  u.ci = u.nci;
+  u.tot = u.ntot;
+  const int cn = walk_chunk<FWD>(x, u.k + 1);
+  u.nci = x.chunks[cn];
+  u.ntot = chunk_total(x, cn);
 }
 
 // The issue cursor: the walk position whose rows the next DMAs fetch, with the bases of its
-// chunk's rows (set when the cursor enters a chunk; a step's rows are then the soffset t * pitch).
+// chunk's rows (set when the cursor enters a chunk; a step's rows are then the soffset t * pitch)
+// and the next chunk's table entry (loaded a chunk ahead).
 struct IssueCur {
   int k, t;
-  ChunkInfo ci;
+  ChunkInfo ci, nci;
   const bf16* bu;
   const bf16* bv;
   const float* bs;
@@ -152,13 +179,14 @@ __device__ __forceinline__ IssueLanes<PT> issue_lanes(const StateCtx& x, int lan
   return il;
 }
 
-// Enter the issue cursor's chunk: its table entry and the bases of its rows.
+// Enter the issue cursor's chunk u.k (its table entry is u.nci, or loaded here at the first
+// chunk): the bases of its rows, and the next chunk's entry.
 template <int PT, bool FWD>
-__device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<PT>& il, IssueCur& u) {
+__device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<PT>& il, IssueCur& u, bool first) {
   const SsdDims& d = x.d;
-  const int kc = min(u.k, x.nch - 1);
-  const int c = __builtin_amdgcn_readfirstlane(FWD ? x.c0 + kc : x.c1 - 1 - kc);
-  u.ci = x.chunks[c];
+  const int c = walk_chunk<FWD>(x, u.k);
+  u.ci = first ? x.chunks[c] : u.nci;
+  u.nci = x.chunks[walk_chunk<FWD>(x, u.k + 1)];
   u.bu = x.U + (int64_t)u.ci.row0 * x.urow + x.ucol;
   u.bv = x.V + (int64_t)u.ci.row0 * x.vrow + x.vcol;
   u.bs = x.fac + ((int64_t)c * d.H + x.h) * d.Qpad;
@@ -201,7 +229,7 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
     if (u.t >= u.ci.len) {
       ++u.k;
       u.t = 0;
-      issue_fetch<PT, FWD>(x, il, u);
+      issue_fetch<PT, FWD>(x, il, u, false);
     }
   }
 }
@@ -213,8 +241,8 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
 template <int PT, bool FWD>
 __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
                                            unsigned char* __restrict__ nxt,
-                                           bf16* __restrict__ tw, bf16* __restrict__ hbw, float* __restrict__ red,
-                                           const IssueLanes<PT>& il, IssueCur& ui, Cursor& uc, float& tot, int& st,
+                                           bf16* __restrict__ tw, bf16* __restrict__ hbw,
+                                           const IssueLanes<PT>& il, IssueCur& ui, Cursor& uc, int& st,
                                            int& s_start, floatx16& acc, floatx16& run) {
   using Cfg = StateCfg<PT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
@@ -298,6 +326,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   ++st;
   if (t0 >= clen) {
     // end of chunk c
+    const float tot = uc.tot;
     const float dec = exp_clamp(tot);
     if (!FWD) {
       // the h_in tile's DMAs were issued at the chunk's first step, before the ring DMAs
@@ -313,26 +342,17 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
       for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hbw[state_row<WIDE>(v, lane) * TC + state_col<WIDE>(lane)];
       contrib *= dec * clamp_pass(tot);
       contrib = wave_sum(contrib);
-      if (lane == 0) red[x.w] = contrib;
-      lds_barrier();
-      // one partial per 32-wide n tile: the PT waves of a 32 x 32 column, or the two 16-wide waves
-      if constexpr (WIDE) {
-        if (x.nt_ok && (x.w & 1) == 0 && lane == 0)
-          x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn + x.nt] = red[x.w] + red[x.w + 1];
-      } else if (x.nt_ok && x.pt == 0 && lane == 0) {
-        float sum = 0.0f;
-        for (int q = 0; q < PT; ++q) sum += red[x.ntl * PT + q];
-        x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn + x.nt] = sum;
-      }
+      // one partial per wave, (32-wide n tile, p tile or 16-wide half) in order: no block
+      // synchronisation at the chunk's end, and the reader sums them in a fixed order
+      const int part = x.nt * PT + (WIDE ? (x.w & 1) : x.pt);
+      if (x.nt_ok && lane == 0) x.dtot_part[((int64_t)c * d.H + x.h) * x.NTn * PT + part] = contrib;
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) run[v] = dec * run[v] + acc[v];
     zero(acc);
     ++uc.k;
     t0 = 0;
-    // the next chunk's entry and total log-decay, a step ahead of their use
-    cursor_fetch<FWD>(x, uc);
-    tot = x.cs[((int64_t)uc.c * d.H + x.h) * d.Qpad + d.Qpad - 1];
+    cursor_next<FWD>(x, uc);
   }
 }
 
@@ -351,7 +371,6 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* s_tile = reinterpret_cast<bf16*>(smem + Cfg::R * SLOT);          // [NW][TWE] state tiles
   bf16* hb = s_tile + Cfg::NW * Cfg::TWE;                                 // [NW][1024] (backward: h_in)
-  float* red = reinterpret_cast<float*>(hb + (FWD ? 0 : Cfg::NW * 1024)); // [NW]
 
   // block -> (n tile pair, unit = (head, sequence)); the pairs of a unit share an XCD
   StateCtx x;
@@ -413,12 +432,10 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
 
   const IssueLanes<PT> il = issue_lanes<PT, FWD>(x, lane);
   IssueCur ui{};                  // issue cursor
-  Cursor uc{0, 0, 0, {}};         // compute cursor
-  float tot = 0.0f;               // total log-decay of the compute cursor's chunk
+  Cursor uc{};                    // compute cursor
   if (x.nch > 0) {  // (an empty sequence passes its state through)
-    issue_fetch<PT, FWD>(x, il, ui);
-    cursor_fetch<FWD>(x, uc);
-    tot = cs[((int64_t)uc.c * d.H + x.h) * d.Qpad + d.Qpad - 1];
+    issue_fetch<PT, FWD>(x, il, ui, true);
+    cursor_init<FWD>(x, uc);
     state_issue<PT, FWD>(x, il, smem, ui, lane);
     state_issue<PT, FWD>(x, il, smem + SLOT, ui, lane);
   }
@@ -431,7 +448,7 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
     wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
     lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
-    state_step<PT, FWD>(x, cur, nxt, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, red, il, ui, uc, tot, st,
+    state_step<PT, FWD>(x, cur, nxt, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, il, ui, uc, st,
                         s_start, acc, run);
   };
   while (uc.k < x.nch) {
@@ -460,7 +477,8 @@ bool state_fused_supported(int dtype, const SsdDims& d) {
   return dtype == 1 && d.P % 8 == 0 && d.N % 8 == 0 && d.vec_x && d.vec_bc;
 }
 
-int state_fused_slices(const SsdDims& d) { return d.Npad / 32; }
+// dtot partials per (chunk, head) of the backward walk: one per wave, i.e. per 32 x 32 tile
+int state_fused_slices(const SsdDims& d) { return d.Npad / 32 * (d.Ppad / 32); }
 
 template <int PT, bool FWD>
 static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* fac,

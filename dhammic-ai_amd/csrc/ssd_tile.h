@@ -257,10 +257,15 @@ __device__ __forceinline__ void tstage_load_f32(TileStage<ROWS, W, NTHR>& s, con
 // 16-byte granules of each row are permuted instead of padding the rows.
 // ---------------------------------------------------------------------------
 // Permuted granule of logical granule g in row r of a W-wide bf16 tile.
-// Tiles read with ds_read_b64_tr_b16 (four rows, two granules per 16 lanes):
+// Tiles read with ds_read_b64_tr_b16 (four rows, two granules per 16 lanes).
+// Rows r and r ^ 1 sit in opposite halves of the LDS's 256-byte bank window,
+// so (r & 3) alone spreads four rows of 32 lanes over all 64 banks. Bit 3 of r
+// is for the 16 x 16 x 32 operand, whose 16-lane groups read rows k .. k + 3
+// and k + 8 .. k + 11 in one half-wave: without it the two groups hit the same
+// banks (a 32-wide read keeps bit 3 fixed over a half-wave and is unaffected).
 template <int W>
 __device__ __forceinline__ int swz_tr(int r, int g) {
-  return W >= 64 ? g ^ ((r & 3) << 1) : g;
+  return W >= 64 ? g ^ ((r & 3) << 1) ^ ((r >> 2) & 2) : g;
 }
 // Tiles read by rows (16 consecutive rows at one granule):
 template <int W>
