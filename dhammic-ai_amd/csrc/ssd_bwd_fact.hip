@@ -30,12 +30,15 @@
 // (s half w % 2, l half (w / 2) % 2) of the tiles (j + t, j) with t = w / 4 + 2 u
 // for dS, rowG and colG (S^T of those two tiles kept in fp32 registers, built
 // once per block), waves 8-11 own dX^T tile (p tile (w / 2) % 2, s half w % 2)
-// over all l and finish the head's tokens. While a head is staged the dS waves
-// write its S'^T = f_l S^T tiles to LDS in bf16 from their registers, so every
-// dy row is staged once, unscaled, for both roles. The next head's inputs, and
-// cs / dt at the rows l each dS lane owns and at the token each dX lane
-// finishes, are loaded into registers while a head computes; a head's dx rows
-// and per-token sums go out through LDS while the next head is staged.
+// over all l and finish the head's tokens. S^T is staged once per block, in
+// bf16, for the dX waves, which scale it by f_l as they read it; every dy row is
+// staged once, unscaled, for both roles. Each role runs its own copy of the head
+// loop (two barriers per head) and loads part of the next head into registers
+// while a head computes: the dX waves the x rows and the per-token scalars
+// (before their contraction), the dS waves the dy rows and dst (after theirs,
+// when their work registers are free). A head's dx rows and per-token sums go
+// out through LDS buffers of the head's parity, flushed by the dS waves while
+// the dX waves compute the next head.
 #include "ssd_launch.h"
 #include "ssd_tile.h"
 
@@ -73,49 +76,52 @@ template <int PT, int NT>
 struct BwdFactLds {
   static constexpr int PP = 32 * PT, NP = 32 * NT;
   static constexpr int XT = tsize<64, PP>(), SQ = tsize<64, 64>(), DT = tsize<PP, NP>(), BT = tsize<64, NP>();
-  static constexpr int RED = 1152 + 128 * kSetW + 256;
-  // bf16: xu, ot, dyr[4], St[4], dstT, Bt; fp32: reductions and the v_s row factors
-  static size_t bytes(int) { return 2 * (size_t)((2 + kSlots) * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
+  // one head's per-token reductions: red_e [2 pt][64], red_x [2 pt][64], red_d [4] (64 reserved),
+  // red_row [kSlots][2 wr][64], red_col [kSetW][2 wc][64]
+  static constexpr int PB = 320 + 128 * kSlots + 128 * kSetW;
+  static constexpr int RED = 2 * PB + 64 + 256;  // by head parity; + v_s and f_l rows of the current head
+  // bf16: xu, ot[2], dyr[4], St[4], dstT, Bt; fp32: reductions and the row factors
+  static size_t bytes(int) { return 2 * (size_t)((3 + kSlots) * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
 };
 
-// One register array serves both roles (roles are fixed per wave): a dS wave keeps the S^T and
-// dS quadrants of its kNsw tiles in it (entries 4 u .. 4 u + 3 and 4 (kNsw + u) .. + 3), a dX wave
-// the next head's tiles, loaded while the current head computes and staged to LDS by the 4 dX
-// waves (x rows, dy rows of the kSlots row blocks, dst). Carried through the head loop as one
-// array, it costs the registers of the larger use instead of both.
+// Register array of a role's head loop: a dS wave keeps the S^T and dS quadrants of its kNsw
+// tiles in it (entries 4 u .. 4 u + 3 and 4 (kNsw + u) .. + 3), a dX wave the next head's x rows.
 constexpr int kUR = 8 * kNsw;
-constexpr int kXThr = 256;  // dX-wave threads that stage a head
+constexpr int kXThr = 256;                 // dX-wave threads: x rows of a head
+constexpr int kYThr = 64 * kDsWaves;       // dS-wave threads: dy rows and dst of a head
 
-template <int ROWS, int W>
+template <int ROWS, int W, int NT = kXThr>
 struct XTile {
   static constexpr int NVEC = ROWS * W / 8;
-  static constexpr int PER = (NVEC + kXThr - 1) / kXThr;
+  static constexpr int PER = (NVEC + NT - 1) / NT;
 };
 
 // Tile rows [0, nrows) and columns [0, width) of a row-major bf16 tensor at g into R[0 .. PER);
 // zeros elsewhere (buffer range check). xt: this thread's index among the staging threads. Every
 // piece is loaded unconditionally (a masked piece reads zeros), so each register is always
 // written by its load and the compiler needs no copy that would wait for the load.
-template <int ROWS, int W>
+template <int ROWS, int W, int NT = kXThr>
 __device__ __forceinline__ void xt_load(u32x4* R, int xt, const bf16* __restrict__ g, int64_t ld, int nrows,
                                         int width) {
   constexpr int CPR = W / 8;
+  using XT = XTile<ROWS, W, NT>;
   const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g);
 #pragma unroll
-  for (int q = 0; q < XTile<ROWS, W>::PER; ++q) {
-    const int id = xt + q * kXThr;
+  for (int q = 0; q < XT::PER; ++q) {
+    const int id = xt + q * NT;
     const int r = id / CPR, k = (id % CPR) * 8;
-    const bool ok = (XTile<ROWS, W>::NVEC % kXThr == 0 || id < XTile<ROWS, W>::NVEC) && r < nrows && k < width;
+    const bool ok = (XT::NVEC % NT == 0 || id < XT::NVEC) && r < nrows && k < width;
     R[q] = __builtin_bit_cast(u32x4, buf_ld16(rs, (int)(((int64_t)r * ld + k) * 2), ok));
   }
 }
-template <int ROWS, int W>
+template <int ROWS, int W, int NT = kXThr>
 __device__ __forceinline__ void xt_store(const u32x4* R, int xt, bf16* t) {
   constexpr int CPR = W / 8;
+  using XT = XTile<ROWS, W, NT>;
 #pragma unroll
-  for (int q = 0; q < XTile<ROWS, W>::PER; ++q) {
-    const int id = xt + q * kXThr;
-    if (XTile<ROWS, W>::NVEC % kXThr == 0 || id < XTile<ROWS, W>::NVEC) {
+  for (int q = 0; q < XT::PER; ++q) {
+    const int id = xt + q * NT;
+    if (XT::NVEC % NT == 0 || id < XT::NVEC) {
       const int r = id / CPR, k = (id % CPR) * 8;
       *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = __builtin_bit_cast(bf16x8, R[q]);
     }
@@ -197,19 +203,24 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   const int64_t brow = (int64_t)d.G * d.N, xrow = (int64_t)d.H * d.P;
 
   bf16* xu = reinterpret_cast<bf16*>(smem);  // x rows of block j          [64][PP]
-  bf16* ot = xu + XT;                        // dx rows of block j         [64][PP]
-  bf16* dyr = ot + XT;                       // dy rows of blocks j + t    [4][64][PP] (slot 0: block j)
+  bf16* ot2 = xu + XT;                       // dx rows of block j         [2 head parity][64][PP]
+  bf16* dyr = ot2 + 2 * XT;                  // dy rows of blocks j + t    [4][64][PP] (slot 0: block j)
   bf16* St = dyr + kSlots * XT;              // S'^T tiles (j + t, j)      [4][64 s][64 l], per head
   bf16* dstT = St + kSlots * SQ;             // dst                        [PP][NP]
   bf16* Bt = dstT + LD::DT;                  // B rows of block j          [64][NP]
   float* red = reinterpret_cast<float*>(Bt + LD::BT);
-  float* red_e = red;           // [2 pt][64]
-  float* red_x = red + 128;     // [2 pt][64]
-  float* red_d = red + 256;     // [4 dX waves]
-  float* vrow = red + 320;      // [64] v_s = dt_s g_s of the current head (0 for a flagged head)
-  float* red_row = red + 384;   // [4 slots][2 wr][64]
-  float* red_col = red + 896;   // [kSetW][2 wc][64]
-  float* frow = red_col + 128 * kSetW;  // [256] f_l = exp(cs_l - c_j) at rows 64 j + l of the current head
+  // A head's per-token results (reductions and dx rows) sit in the buffers of its parity: the dS
+  // waves flush head k - 1 while head k computes, and head k + 1 reuses them after two barriers.
+  struct HeadBuf {
+    float *e, *x, *d, *row, *col;
+    bf16* ot;
+  };
+  auto hbuf = [&](int k) {
+    float* r = red + (k & 1) * LD::PB;
+    return HeadBuf{r, r + 128, r + 256, r + 320, r + 320 + 128 * kSlots, ot2 + (k & 1) * XT};
+  };
+  float* vrow = red + 2 * LD::PB;  // [64] v_s = dt_s g_s of the current head (0 for a flagged head)
+  float* frow = vrow + 64;         // [256] f_l = exp(cs_l - c_j) at rows 64 j + l of the current head
 
   // ---- B rows of block j; the dS waves' S^T quadrants of tiles (j + t, j), t = ws + kSetW u: rows s
   // (block j), columns l (block j + t), kept in fp32 registers for every head ----
@@ -258,18 +269,22 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
 
   // dX-wave tile pieces in UR: x rows, dy rows of row block j + t, dst
   using TX = XTile<64, PP>;
-  using TD = XTile<PP, NP>;
-  constexpr int oX = 0, oY = TX::PER, oD = TX::PER * (1 + kSlots);
-  static_assert(oD + TD::PER <= kUR, "dX staging registers");
+  using TY = XTile<64, PP, kYThr>;
+  using TS = XTile<PP, NP, kYThr>;
+  constexpr int oX = 0;
+  static_assert(TX::PER <= kUR, "dX staging registers");
+  // the dS waves' pieces of the next head: dy rows of row blocks j .. j + kSlots - 1, then dst
+  constexpr int oS = kSlots * TY::PER, nYR = oS + TS::PER;
+  u32x4 YR[nYR];
+#pragma unroll
+  for (int q = 0; q < nYR; ++q) YR[q] = u32x4{0u, 0u, 0u, 0u};
   BwdFactScalars hs{};  // loaded by the dX waves; zero (unused) in the dS waves
   const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);  // token this lane finishes (dX waves)
   // dt as used: the loaded value where the token exists and dt is given, else 1
   auto dt_use = [&](float v, int tok) { return (d.has_dt && tok < ci.len) ? v : 1.0f; };
-  // The next head's loads, issued by the dX waves only (the dS waves read what they need of a head
-  // from LDS and issue no global load in the head loop, so no load of theirs is ever pending where
-  // the dX waves reuse registers). All are unconditional masked buffer loads used only after the
-  // staging barrier, and every per-lane offset derives from an opaque thread id recomputed per head
-  // (held across the head loop, these offsets spill, and their reloads wait for the prefetch).
+  // The dX waves' loads of the next head. All are unconditional masked buffer loads used only after
+  // the staging barrier, and every per-lane offset derives from an opaque thread id recomputed per
+  // head (held across the head loop, these offsets spill, and their reloads wait for the prefetch).
   auto load_head = [&](int h) {
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
@@ -291,21 +306,35 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     hs.fast = __float_as_int(buf_ldf(buf_rsrc(a.fast + (int64_t)c * d.H), h * 4, true));
     const int64_t xo = (int64_t)h * d.P;
     xt_load<64, PP>(UR + oX, xt, a.x + (int64_t)(ci.row0 + 64 * j) * xrow + xo, xrow, min(64, ci.len - 64 * j), d.P);
+  };
+  // The next head's dy rows and dst, loaded by the dS waves once their tiles of the current head are
+  // done (their registers are then free, and they would otherwise wait at the head's end for the dX
+  // waves); staged by them with the next head. Same masking as load_head.
+  auto load_dy = [&](int h) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int64_t xo = (int64_t)h * d.P;
 #pragma unroll
     for (int t = 0; t < kSlots; ++t) {
       // row blocks past the chunk read zeros (from the chunk's first row, so the base stays inside dy)
       const bool tv = t < nt_i;
-      xt_load<64, PP>(UR + oY + TX::PER * t, xt, a.dy + (int64_t)(ci.row0 + (tv ? 64 * (j + t) : 0)) * xrow + xo,
-                      xrow, tv ? min(64, ci.len - 64 * (j + t)) : 0, d.P);
+      xt_load<64, PP, kYThr>(YR + TY::PER * t, tid, a.dy + (int64_t)(ci.row0 + (tv ? 64 * (j + t) : 0)) * xrow + xo,
+                             xrow, tv ? min(64, ci.len - 64 * (j + t)) : 0, d.P);
     }
-    xt_load<PP, NP>(UR + oD, xt, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    xt_load<PP, NP, kYThr>(YR + oS, tid, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
   };
-  // per-token results of head h (from the reduction buffers) and its dx rows (from ot)
-  // Run by the dS waves only (threads 0 .. 64 kDsWaves - 1), while the dX waves stage the next head.
+  // head order rotated per chunk: the resident blocks then read different 128-byte columns of the 8 KB
+  // token rows at any moment instead of all the same one (HBM channel spread)
+  const int nh = h_hi - h_lo, hrot = c % nh;
+  auto head = [&](int k) { const int m = k + hrot; return h_lo + (m >= nh ? m - nh : m); };
+  // per-token results of head h, the k-th of the block (from its parity's reduction buffers and dx rows)
+  // Run by the dS waves only (threads 0 .. 64 kDsWaves - 1), while the dX waves compute the next head.
   // (thread offsets come from an opaque thread id recomputed per head: held across the head loop they
   // spill, and each reload waits for every outstanding load and store of the wave)
   constexpr int kFl = 64 * kDsWaves;
-  auto flush = [&](int h) {
+  auto flush = [&](int k) {
+    const int h = head(k);
+    const HeadBuf b = hbuf(k);
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int64_t hq = ((int64_t)c * d.H + h) * Qpad;
@@ -314,10 +343,10 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
       if (tg < ci.len) {
         float cg = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 2 * kSetW; ++q) cg += red_col[64 * q + tl];
+        for (int q = 0; q < 2 * kSetW; ++q) cg += b.col[64 * q + tl];
         a.colG[hq + tg] = cg;
-        a.eterm[hq + tg] = red_e[tl] + red_e[64 + tl];
-        a.xdx[hq + tg] = red_x[tl] + red_x[64 + tl];
+        a.eterm[hq + tg] = b.e[tl] + b.e[64 + tl];
+        a.xdx[hq + tg] = b.x[tl] + b.x[64 + tl];
       }
     }
     for (int e = tid; e < nt_i * 64; e += kFl) {
@@ -325,54 +354,40 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
       const int lg = 64 * (j + t) + l;
       if (lg < ci.len)
         a.rowG[((int64_t)j * d.max_chunks + c) * d.H * (int64_t)Qpad + (int64_t)h * Qpad + lg] =
-            red_row[(t * 2 + 0) * 64 + l] + red_row[(t * 2 + 1) * 64 + l];
+            b.row[(t * 2 + 0) * 64 + l] + b.row[(t * 2 + 1) * 64 + l];
     }
-    if (tid == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = red_d[0] + red_d[1] + red_d[2] + red_d[3];
+    if (tid == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = b.d[0] + b.d[1] + b.d[2] + b.d[3];
     constexpr int CPR = PP / 8;
 #pragma unroll
     for (int id = tid; id < 64 * CPR; id += kFl) {
-      const int r = id / CPR, k = (id % CPR) * 8;
-      if (64 * j + r < ci.len && k < d.P && MODE != 2)
-        *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + k) =
-            tld8<PP>(ot, r, k);
+      const int r = id / CPR, kk = (id % CPR) * 8;
+      if (64 * j + r < ci.len && kk < d.P && MODE != 2)
+        *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + kk) =
+            tld8<PP>(b.ot, r, kk);
     }
   };
 
-  // head order rotated per chunk: the resident blocks then read different 128-byte columns of the 8 KB
-  // token rows at any moment instead of all the same one (HBM channel spread)
-  const int nh = h_hi - h_lo, hrot = c % nh;
-  auto head = [&](int k) { const int m = k + hrot; return h_lo + (m >= nh ? m - nh : m); };
-  if (xrole) load_head(head(0));
-  for (int k = 0; k < nh; ++k) {
-    lane = opaque_lane();
-    hh = lane >> 5;
-    l32 = lane & 31;
-    // previous head: LDS reads done, reductions and ot complete (LDS only: the previous
-    // head's global stores and this head's prefetch stay in flight)
-    lds_barrier();
-    // this head's per-token values for the finishing step (hs is reloaded below)
-    const bool ok = hs.fast != 0;
-    const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = dt_use(hs.edt, te);
-    const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
-    const float Dh = hs.D;
-    if (xrole) {
+  // Each role runs its own copy of the head loop: the two meet at the same two barriers per head,
+  // and the registers one role carries from head to head (the dS waves' tiles and dy rows, the
+  // dX waves' next-head pieces) are not held through the other role's code.
+  if (!xrole) {
+    load_dy(head(0));
+    for (int k = 0; k < nh; ++k) {
+      lane = opaque_lane();
+      hh = lane >> 5;
+      l32 = lane & 31;
+      // previous head: LDS reads done, its dx rows and reductions complete (LDS only: the
+      // global stores of the head before and the loads of this one stay in flight)
+      lds_barrier();
       int tid = threadIdx.x;
       asm volatile("" : "+v"(tid));
-      const int xt = tid - 64 * kDsWaves;
-      xt_store<64, PP>(UR + oX, xt, xu);
 #pragma unroll
       for (int t = 0; t < kSlots; ++t)
-        if (t < nt_i) xt_store<64, PP>(UR + oY + TX::PER * t, xt, dyr + t * XT);
-      xt_store<PP, NP>(UR + oD, xt, dstT);
-      // f_l of rows 64 j + xt and v_s of the head's tokens s (block j); zero for a flagged head
-      frow[xt] = (ok && xt < 64 * nt_i) ? exp2_fast(hs.fcs * SSD_LOG2E - e_cj2) : 0.0f;
-      if (pt == 0 && hh == 0) vrow[32 * sr + l32] = ok ? e_dt * exp2_fast(e_cj2 - e_c2) : 0.0f;
-    } else if (k > 0) {
-      flush(head(k - 1));  // its LDS (ot, reductions) is not touched by the staging above
-    }
-    lds_barrier();
+        if (t < nt_i) xt_store<64, PP, kYThr>(YR + TY::PER * t, tid, dyr + t * XT);
+      xt_store<PP, NP, kYThr>(YR + oS, tid, dstT);
+      lds_barrier();
+      const HeadBuf hb = hbuf(k);
 
-    if (!xrole) {
       // ---- tiles (j + t, j): P = x dy^T (quadrant, exact), then in fp32
       // dS += f_l v_s P, G = S f_l v_s P, rowG (over s: registers), colG (over l: across lanes) ----
       float vs[16];
@@ -403,22 +418,50 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           }
           ur_set(UR + 4 * (kNsw + uu), dSq);
           rs = add_xor32(rs);
-          if (hh == 0) red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
+          if (hh == 0) hb.row[(t * 2 + wr) * 64 + 32 * wc + l32] = rs;
           colp += half_reduce16(G, lane);
         } else if (hh == 0) {
-          red_row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
+          hb.row[(t * 2 + wr) * 64 + 32 * wc + l32] = 0.0f;
         }
       }
-      if ((l32 & 1) == 0) red_col[(ws * 2 + wc) * 64 + 32 * wr + acc_row((l32 >> 1) & 15, lane)] = colp;
-    } else {
+      if ((l32 & 1) == 0) hb.col[(ws * 2 + wc) * 64 + 32 * wr + acc_row((l32 >> 1) & 15, lane)] = colp;
+      if (k + 1 < nh) load_dy(head(k + 1));
+      // the previous head's results, complete since this head's first barrier: written out while the
+      // dX waves still compute, instead of in the staging phase both roles wait on
+      if (k > 0) flush(k - 1);
+    }
+  } else {
+    load_head(head(0));
+    for (int k = 0; k < nh; ++k) {
+      lane = opaque_lane();
+      hh = lane >> 5;
+      l32 = lane & 31;
+      // previous head: LDS reads done, its dx rows and reductions complete (LDS only: this
+      // head's loads stay in flight)
+      lds_barrier();
+      // this head's per-token values for the finishing step (hs is reloaded below)
+      const bool ok = hs.fast != 0;
+      const float e_c2 = hs.ecs * SSD_LOG2E, e_dt = dt_use(hs.edt, te);
+      const float e_cj2 = hs.cj * SSD_LOG2E, e_cl2 = hs.cl * SSD_LOG2E;
+      const float Dh = hs.D;
+      int tid = threadIdx.x;
+      asm volatile("" : "+v"(tid));
+      const int xt = tid - 64 * kDsWaves;
+      xt_store<64, PP>(UR + oX, xt, xu);
+      // f_l of rows 64 j + xt and v_s of the head's tokens s (block j); zero for a flagged head
+      frow[xt] = (ok && xt < 64 * nt_i) ? exp2_fast(hs.fcs * SSD_LOG2E - e_cj2) : 0.0f;
+      if (pt == 0 && hh == 0) vrow[32 * sr + l32] = ok ? e_dt * exp2_fast(e_cj2 - e_c2) : 0.0f;
+      lds_barrier();
+      const HeadBuf hb = hbuf(k);
+
       if (k + 1 < nh) load_head(head(k + 1));
       if (pt >= PT) {
         // dX waves past the p tiles add zeros
         if (hh == 0) {
-          red_e[pt * 64 + 32 * sr + l32] = 0.0f;
-          red_x[pt * 64 + 32 * sr + l32] = 0.0f;
+          hb.e[pt * 64 + 32 * sr + l32] = 0.0f;
+          hb.x[pt * 64 + 32 * sr + l32] = 0.0f;
         }
-        if (lane == 0) red_d[w - kDsWaves] = 0.0f;
+        if (lane == 0) hb.d[w - kDsWaves] = 0.0f;
       } else {
         // ---- dX^T += dy^T S' over the tiles (j + t, j), S'[l][s] = f_l S[l][s] scaled in registers;
         // state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
@@ -463,21 +506,21 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
             dsum = fmaf(xf, yf, dsum);
             o[e] = (bf16)fmaf(dts, dX, Dh * yf);
           }
-          *reinterpret_cast<bf16x4*>(ot + toff<PP>(s_loc, p0)) = o;
+          *reinterpret_cast<bf16x4*>(hb.ot + toff<PP>(s_loc, p0)) = o;
         }
         esum = add_xor32(esum);
         xsum = add_xor32(xsum);
         dsum = wave_sum(dsum);
         if (hh == 0) {
-          red_e[pt * 64 + s_loc] = esum * dts * pw;
-          red_x[pt * 64 + s_loc] = xsum;
+          hb.e[pt * 64 + s_loc] = esum * dts * pw;
+          hb.x[pt * 64 + s_loc] = xsum;
         }
-        if (lane == 0) red_d[w - kDsWaves] = dsum;
+        if (lane == 0) hb.d[w - kDsWaves] = dsum;
       }
     }
   }
   __syncthreads();
-  flush(head(nh - 1));
+  flush(nh - 1);
 
   // ---- dS tiles, summed over the slice's heads (zero outside the causal mask) ----
   if (xrole || MODE == 2) return;
