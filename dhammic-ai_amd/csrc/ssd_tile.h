@@ -355,18 +355,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return add_xor32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
 }
 
+// Value of x at lane L ^ m within each 16-lane row, for the DPP controls below.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
 // Sum of v over the 32 lanes of each half-wave, for 16 values at once.
 // Afterwards lane L returns the sum of v[(L >> 1) & 15] over its half.
+// A butterfly that halves the values at every stage, the lane's bit of the
+// stage choosing the half it keeps; all of it in VALU, with no LDS round trip:
+// lanes L ^ 16 by v_permlane16_swap (the odd rows of its first operand trade
+// places with the even rows of its second, so one add completes a pair), then
+// DPP within rows: L ^ 8 (row_ror:8), L ^ 7 (row_half_mirror, which pairs lanes
+// of opposite bit 2 as L ^ 4 would and keeps the summed lane sets disjoint),
+// L ^ 2 and L ^ 1 (quad_perm).
 __device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
   float a[8];
-  {
-    const bool b = (L >> 4) & 1;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float send = b ? v[k] : v[k + 8];
-      const float keep = b ? v[k + 8] : v[k];
-      a[k] = keep + __shfl_xor(send, 16, 64);
-    }
+  for (int k = 0; k < 8; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 8]), false, false);
+    a[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   float c[4];
   {
@@ -375,7 +384,7 @@ __device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
     for (int k = 0; k < 4; ++k) {
       const float send = b ? a[k] : a[k + 4];
       const float keep = b ? a[k + 4] : a[k];
-      c[k] = keep + __shfl_xor(send, 8, 64);
+      c[k] = keep + dpp_f<0x128>(send);  // row_ror:8
     }
   }
   float e[2];
@@ -385,7 +394,7 @@ __device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
     for (int k = 0; k < 2; ++k) {
       const float send = b ? c[k] : c[k + 2];
       const float keep = b ? c[k + 2] : c[k];
-      e[k] = keep + __shfl_xor(send, 4, 64);
+      e[k] = keep + dpp_f<0x141>(send);  // row_half_mirror
     }
   }
   float f;
@@ -393,7 +402,7 @@ __device__ __forceinline__ float half_reduce16(float (&v)[16], int L) {
     const bool b = (L >> 1) & 1;
     const float send = b ? e[0] : e[1];
     const float keep = b ? e[1] : e[0];
-    f = keep + __shfl_xor(send, 2, 64);
+    f = keep + dpp_f<0x4E>(send);  // quad_perm 2,3,0,1
   }
-  return f + __shfl_xor(f, 1, 64);
+  return f + dpp_f<0xB1>(f);  // quad_perm 1,0,3,2
 }
