@@ -197,17 +197,28 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
 
   // ---- per-head loop: the next head's inputs are loaded into registers while one head computes ----
   FactStage<PT, NT, NB> st;
-  auto load_head = [&](int h) {
+  // in two parts, issued before each of the wave's two quadrants: a wave's loads wait for room in
+  // the texture unit's queue, which the first quadrant's contraction then drains, instead of every
+  // wave of the block queueing its whole share before it computes
+  constexpr int NB0 = (NB + 1) / 2;
+  auto load_head = [&](int h, int part) {
+    if (part == 0) {
 #pragma unroll
-    for (int i = 0; i < NB; ++i)
-      tstage_load_v(st.x[i], a.x + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
-                    min(64, ci.len - 64 * i), d.P);
-    tstage_load_v(st.hin, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
-    st.cs = 0.0f;
-    st.dt = 1.0f;
-    if (threadIdx.x < 64 * NB) {
-      st.cs = a.cs[((int64_t)c * d.H + h) * d.Qpad + threadIdx.x];
-      if (d.has_dt && (int)threadIdx.x < ci.len) st.dt = a.dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
+      for (int i = 0; i < NB0; ++i)
+        tstage_load_v(st.x[i], a.x + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
+                      min(64, ci.len - 64 * i), d.P);
+      st.cs = 0.0f;
+      st.dt = 1.0f;
+      if (threadIdx.x < 64 * NB) {
+        st.cs = a.cs[((int64_t)c * d.H + h) * d.Qpad + threadIdx.x];
+        if (d.has_dt && (int)threadIdx.x < ci.len) st.dt = a.dt[(int64_t)(ci.row0 + threadIdx.x) * d.H + h];
+      }
+    } else {
+#pragma unroll
+      for (int i = NB0; i < NB; ++i)
+        tstage_load_v(st.x[i], a.x + (int64_t)(ci.row0 + 64 * i) * xrow + (int64_t)h * d.P, xrow,
+                      min(64, ci.len - 64 * i), d.P);
+      tstage_load_v(st.hin, a.hin + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
     }
   };
   // row scale of token t = threadIdx.x: dt_t * exp(c_j - cs_t); the wave's 64
@@ -217,7 +228,8 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
     const float cj = __shfl(c2, 63, 64);
     if (threadIdx.x < 64 * NB) s_g[buf * 64 * NB + threadIdx.x] = st.dt * exp2_fast(cj - c2);
   };
-  load_head(h_lo);
+  load_head(h_lo, 0);
+  load_head(h_lo, 1);
   put_g(0);
   for (int h = h_lo; h < h_hi; ++h) {
     const int buf = (h - h_lo) & 1;
@@ -246,11 +258,12 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
         if (i >= 0 && lg < ci.len) dtk[q] = a.Dtok[(int64_t)(ci.row0 + lg) * d.H + h];
       }
     }
-    if (h + 1 < h_hi) load_head(h + 1);
+    if (h + 1 < h_hi) load_head(h + 1, 0);
     const float Dh = d.has_D ? a.Dv[h] : 0.0f;
 
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
+      if (q == 1 && h + 1 < h_hi) load_head(h + 1, 1);
       const int i = q == 0 ? QD::i0 : QD::i1, lh = q == 0 ? QD::lh0 : QD::lh1;
       const int nq = q == 0 ? QD::n0 : QD::n1, base = q == 0 ? 0 : QD::n0;
       if (nq == 0) continue;
