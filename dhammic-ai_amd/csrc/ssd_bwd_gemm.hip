@@ -15,7 +15,8 @@
 // slots, so no register holds staged data and the loads of two heads are in
 // flight while one computes. The ring allows one block per CU, so its 8 waves
 // take two roles that share each SIMD and overlap: waves 0-3 build dC and the
-// decay gradient (and issue the ring loads), waves 4-7 build dB. LDS rows are unpadded; 16-byte granules are
+// decay gradient, waves 4-7 build dB (the shorter work) and issue the ring loads,
+// whose issue waits for room in the texture unit's queue. LDS rows are unpadded; 16-byte granules are
 // permuted per row so that transposed reads (h_in, dst) and row reads (x, dy)
 // hit distinct banks.
 #include "ssd_launch.h"
@@ -31,7 +32,7 @@ struct GemmCfg {
   // bytes of one ring slot: h_in, dst, x, dy, then cs, dt, cs_last, spare (64 floats each)
   static constexpr size_t kSlot = (size_t)(2 * HIN + 2 * XT) * 2 + 4 * 256;
   static constexpr size_t bytes = 3 * kSlot;
-  // DMA instructions per issuing wave and head (waves 0-3)
+  // DMA instructions per issuing wave and head (waves 4-7)
   static constexpr int kTileDma = HIN / 512;    // 1 KB per instruction
   static constexpr int kRowDma = XT / 512;
   static constexpr int kPerWave = (2 * kTileDma + 2 * kRowDma) / 4 + 1;
@@ -65,7 +66,8 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const ChunkInfo ci = chunks[c];
   if (64 * kb >= ci.len) return;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool brole = w >= 4;  // dB waves (else dC waves, which also issue the ring loads)
+  const bool brole = w >= 4;  // dB waves, which also issue the ring loads (else dC waves)
+  const int wi = w & 3;       // index among the issuing (dB) waves
   const int th = w & 1, nh = (w >> 1) & 1;
   int lane = threadIdx.x & 63, hh = lane >> 5, l32 = lane & 31;
   const int t_loc = 32 * th + l32;         // token of this lane within block kb
@@ -77,34 +79,34 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   const int h0 = g * d.hpg, h1 = h0 + d.hpg;
 
   // ---- one head's inputs into a ring slot (kPerWave DMA instructions per issuing wave) ----
-  // Waves 0-1 load h_in and the x rows, waves 2-3 dst and the dy rows, each its own fixed share, and
-  // one scalar row each (wave 0 cs of the block's tokens, wave 1 dt, wave 2 cs of the chunk's last
-  // position, wave 3 gamma in trapezoidal mode). Every per-lane offset and every base is fixed for
+  // Issuing waves 0-1 (waves 4-5) load h_in and the x rows, 2-3 dst and the dy rows, each its own fixed
+  // share, and one scalar row each (0 cs of the block's tokens, 1 dt, 2 cs of the chunk's last position,
+  // 3 gamma in trapezoidal mode). Every per-lane offset and every base is fixed for
   // the block; a head only moves the bases by a wave-uniform soffset.
   constexpr int TPW = Cfg::kTileDma / 2, RPW = Cfg::kRowDma / 2;  // tile / row DMAs per issuing wave
   constexpr int TG = NP / 8, TRI = 64 / TG;  // h_in / dst rows of NP elements: granules per row, rows per DMA
   constexpr int XG = PP / 8, XRI = 64 / XG;  // x / dy rows of PP elements
-  const bool second = w >= 2;
+  const bool second = wi >= 2;
   int vt[TPW], vr[RPW];
 #pragma unroll
   for (int q = 0; q < TPW; ++q) {
-    const int qi = (w & 1) * TPW + q, r = qi * TRI + lane / TG;
+    const int qi = (wi & 1) * TPW + q, r = qi * TRI + lane / TG;
     vt[q] = (r * NP + (swz_tr<NP>(r, lane % TG) << 3)) * 2;
   }
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
-    const int qi = (w & 1) * RPW + q, r = qi * XRI + lane / XG;
+    const int qi = (wi & 1) * RPW + q, r = qi * XRI + lane / XG;
     const int gcol = swz_nat<PP>(r, lane % XG) << 3;
     vr[q] = (r < nrows && gcol < d.P) ? (int)((r * xrow + gcol) * 2) : SSD_BUF_SIZE;
   }
   const int64_t row_b = (int64_t)(ci.row0 + 64 * kb);
   const bf16* tile_base = (second ? dst : hin) + (int64_t)c * d.H * Cfg::HIN;
   const bf16* rows_base = (second ? dy : x) + row_b * xrow;
-  const bool s_tok = (w == 1 && d.has_dt) || (w == 3 && d.trapz);  // a per-token [R][H] row
-  const float* scal_base = w == 1 && d.has_dt ? dt + row_b * d.H
-                         : w == 3 && d.trapz ? tz_gam + row_b * d.H : cs + (int64_t)c * d.H * Qpad;
+  const bool s_tok = (wi == 1 && d.has_dt) || (wi == 3 && d.trapz);  // a per-token [R][H] row
+  const float* scal_base = wi == 1 && d.has_dt ? dt + row_b * d.H
+                         : wi == 3 && d.trapz ? tz_gam + row_b * d.H : cs + (int64_t)c * d.H * Qpad;
   const int s_vo = s_tok ? (lane < nrows ? lane * d.H * 4 : SSD_BUF_SIZE)
-                 : w == 0 ? (64 * kb + lane) * 4 : w == 1 ? SSD_BUF_SIZE : (Qpad - 1) * 4;
+                 : wi == 0 ? (64 * kb + lane) * 4 : wi == 1 ? SSD_BUF_SIZE : (Qpad - 1) * 4;
   const int s_str = s_tok ? 4 : Qpad * 4;  // soffset bytes per head
   auto issue = [&](int h, unsigned char* base) {
     const __amdgpu_buffer_rsrc_t rt = buf_rsrc(tile_base), rr = buf_rsrc(rows_base), rs = buf_rsrc(scal_base);
@@ -115,19 +117,19 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
 #pragma unroll
     for (int q = 0; q < TPW; ++q) {
       const int vo = vt[q];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(bt + ((w & 1) * TPW + q) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(bt + ((wi & 1) * TPW + q) * 1024),
                                                16, vo, so_t, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
       const int vo = vr[q];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(br + ((w & 1) * RPW + q) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(br + ((wi & 1) * RPW + q) * 1024),
                                                16, vo, so_r, 0, 0);
     }
     {
       const int vo = s_vo, so = h * s_str;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(base + (2 * Cfg::HIN + 2 * Cfg::XT) * 2 + w * 256), 4, vo, so, 0,
+          rs, (__attribute__((address_space(3))) void*)(base + (2 * Cfg::HIN + 2 * Cfg::XT) * 2 + wi * 256), 4, vo, so, 0,
           0);
     }
   };
@@ -159,7 +161,7 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   // rows at any moment instead of all the same one (HBM channel spread)
   const int nhd = h1 - h0, hrot = c % nhd;
   auto head = [&](int k) { const int m = k + hrot; return h0 + (m >= nhd ? m - nhd : m); };
-  if (!brole) {
+  if (brole) {
     issue(head(0), smem);
     if (1 < nhd) issue(head(1), smem + Cfg::kSlot);
   }
@@ -168,12 +170,12 @@ __global__ void __launch_bounds__(512) k_bwd_gemm(SsdDims d, const ChunkInfo* __
   auto head_step = [&](int k, const unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
     const int h = head(k);
     // this wave's loads of head k are done (those of k + 1 may still fly); then every wave's
-    if (!brole) {
+    if (brole) {
       if (k + 1 < nhd) wait_vm<Cfg::kPerWave>();
       else wait_vm<0>();
     }
     lds_barrier();  // head k visible in LDS; slot (k + 2) % 3 is free (head k - 1 done)
-    ring_step(cur, nxt, !brole && k + 2 < nhd,
+    ring_step(cur, nxt, brole && k + 2 < nhd,
               [&](unsigned char* nxt) { issue(head(k + 2), nxt); }, [&](const unsigned char* base) {
     if (brole && d.da_only) return;  // decay gradient only: no dB
     lane = opaque_lane();
