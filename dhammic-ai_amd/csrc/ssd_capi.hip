@@ -59,6 +59,8 @@ int plan(const ssd_desc_t* s, Plan* p) {
   if (s->chunk > SSD_MAX_CHUNK || s->headdim > SSD_MAX_HEADDIM || s->dstate > SSD_MAX_DSTATE)
     return SSD_ERR_UNSUPPORTED;
   if (s->varlen && s->nseq > kMaxSeq) return SSD_ERR_UNSUPPORTED;
+  // each factor bounded before the products below (which then fit in int64)
+  if (s->batch > INT32_MAX || s->seqlen > INT32_MAX) return SSD_ERR_UNSUPPORTED;
   const int64_t R = s->batch * s->seqlen;
   if (R > INT32_MAX / 2 || s->nheads > kMaxGrid) return SSD_ERR_UNSUPPORTED;
   const int64_t cps = (s->seqlen + s->chunk - 1) / s->chunk;
@@ -349,6 +351,20 @@ void* scratch_on_current_device() {
   return g_scratch_ptr[dev];
 }
 
+// Shape checks of the cache helpers (ssd_materialize_L, ssd_decay_chunk), before their pointers: each
+// extent goes to the launch as an int, and the grid (batch x heads, times the chunks for L) is one
+// dimension; every factor is bounded before a product.
+int cache_helper_shape(const ssd_desc_t* d) {
+  if (!d) return SSD_ERR_INVALID;
+  if (d->batch < 1 || d->seqlen < 1 || d->nheads < 1 || d->chunk < 1 || d->seqlen % d->chunk || d->varlen ||
+      (d->dtype != SSD_DTYPE_F32 && d->dtype != SSD_DTYPE_BF16))
+    return SSD_ERR_INVALID;
+  if (d->batch > INT32_MAX || d->nheads > INT32_MAX || d->seqlen > INT32_MAX) return SSD_ERR_UNSUPPORTED;
+  const int64_t bh = d->batch * d->nheads;
+  if (bh > INT32_MAX || bh * (d->seqlen / d->chunk) > INT32_MAX) return SSD_ERR_UNSUPPORTED;
+  return SSD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -503,11 +519,9 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
 }
 
 int ssd_materialize_L(const ssd_desc_t* desc, const void* a, void* L, void* stream) {
-  if (!desc || !a || !L) return SSD_ERR_INVALID;
-  if (desc->batch < 1 || desc->seqlen < 1 || desc->nheads < 1 || desc->chunk < 1 || desc->seqlen % desc->chunk ||
-      desc->varlen || (desc->dtype != SSD_DTYPE_F32 && desc->dtype != SSD_DTYPE_BF16))
-    return SSD_ERR_INVALID;
-  if (desc->batch * desc->nheads * (desc->seqlen / desc->chunk) > INT32_MAX) return SSD_ERR_UNSUPPORTED;
+  const int st = cache_helper_shape(desc);
+  if (st != SSD_OK) return st;
+  if (!a || !L) return SSD_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
   SSD_TRY(launch_materialize_L(desc->dtype, (int)desc->batch, (int)desc->seqlen, (int)desc->nheads,
                                (int)desc->chunk, a, L, s));
@@ -515,10 +529,9 @@ int ssd_materialize_L(const ssd_desc_t* desc, const void* a, void* L, void* stre
 }
 
 int ssd_decay_chunk(const ssd_desc_t* desc, const void* A_cumsum, void* decay_chunk, void* stream) {
-  if (!desc || !A_cumsum || !decay_chunk) return SSD_ERR_INVALID;
-  if (desc->batch < 1 || desc->seqlen < 1 || desc->nheads < 1 || desc->chunk < 1 || desc->seqlen % desc->chunk ||
-      desc->varlen || (desc->dtype != SSD_DTYPE_F32 && desc->dtype != SSD_DTYPE_BF16))
-    return SSD_ERR_INVALID;
+  const int st = cache_helper_shape(desc);
+  if (st != SSD_OK) return st;
+  if (!A_cumsum || !decay_chunk) return SSD_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
   SSD_TRY(launch_decay_chunk(desc->dtype, (int)desc->batch, (int)desc->nheads, (int)(desc->seqlen / desc->chunk),
                              (int)desc->chunk, A_cumsum, decay_chunk, s));

@@ -1,0 +1,119 @@
+// Host-side fuzz of the C ABI's descriptor validation (ssd_validate, ssd_workspace_bytes, and the shape
+// checks of ssd_materialize_L / ssd_decay_chunk, called with null tensors so that they never launch), built with
+// AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_sanitize_host.py. Edge values of every
+// field, then seeded random descriptors mixing them; each call must return a status of the ABI (or, for
+// the workspace query, 0 exactly when validation fails), and the sanitizers abort on any overflow,
+// out-of-bounds access or invalid enum load. No GPU call is made.
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "ssd_mi355x.h"
+
+namespace {
+
+uint64_t g_state = 0x9E3779B97F4A7C15ull;
+uint64_t next_u64() {  // xorshift64*
+  g_state ^= g_state >> 12;
+  g_state ^= g_state << 25;
+  g_state ^= g_state >> 27;
+  return g_state * 0x2545F4914F6CDD1Dull;
+}
+
+const int64_t kI64[] = {INT64_MIN, INT64_MIN + 1, -1, 0, 1, 2, 3, 7, 8, 31, 32, 33, 63, 64, 65, 127, 128, 129,
+                        255, 256, 257, 4096, 65535, 65536, 1 << 20, INT32_MAX / 2, INT32_MAX / 2 + 1, INT32_MAX,
+                        (int64_t)INT32_MAX + 1, (int64_t)1 << 40, INT64_MAX / 2, INT64_MAX - 255, INT64_MAX};
+const int32_t kI32[] = {INT32_MIN, -1, 0, 1, 2, 3, 4, 7, 8, 16, 255, INT32_MAX};
+const float kF32[] = {-1.0f, -0.0f, 0.0f, 1e-6f, 1.0f, 1e30f, __builtin_inff(), __builtin_nanf("")};
+
+template <class T, size_t N>
+T pick(const T (&a)[N]) { return a[next_u64() % N]; }
+
+ssd_desc_t valid_base() {
+  ssd_desc_t d;
+  std::memset(&d, 0, sizeof(d));
+  d.batch = 2; d.seqlen = 512; d.nheads = 8; d.headdim = 64; d.ngroups = 2; d.dstate = 64; d.chunk = 128;
+  d.dtype = SSD_DTYPE_BF16; d.state_dtype = SSD_DTYPE_F32; d.a_mode = SSD_A_PER_HEAD;
+  d.has_dt = 1; d.has_D = 1; d.norm_eps = 1e-6f;
+  return d;
+}
+
+int check(const ssd_desc_t& d) {
+  const int st = ssd_validate(&d);
+  if (st != SSD_OK && st != SSD_ERR_INVALID && st != SSD_ERR_UNSUPPORTED) {
+    std::fprintf(stderr, "ssd_validate returned %d\n", st);
+    return 1;
+  }
+  // null tensors: a shape that passes is rejected for its pointers, before any launch
+  const int sl = ssd_materialize_L(&d, nullptr, nullptr, nullptr), sd = ssd_decay_chunk(&d, nullptr, nullptr, nullptr);
+  if (sl == SSD_OK || sd == SSD_OK) {
+    std::fprintf(stderr, "cache helper accepted null tensors (%d, %d)\n", sl, sd);
+    return 1;
+  }
+  for (int kind = -1; kind <= 3; ++kind) {
+    const size_t ws = ssd_workspace_bytes(&d, kind);
+    if (st != SSD_OK && ws != 0) {
+      std::fprintf(stderr, "workspace %zu for an invalid descriptor (status %d)\n", ws, st);
+      return 1;
+    }
+  }
+  return 0;
+}
+
+}  // namespace
+
+int main() {
+  int bad = 0;
+  if (ssd_validate(nullptr) != SSD_ERR_INVALID || ssd_workspace_bytes(nullptr, SSD_WS_SAVED) != 0) ++bad;
+  const ssd_desc_t base = valid_base();
+  if (ssd_validate(&base) != SSD_OK) ++bad;
+  // every edge value in every 64-bit field of an otherwise valid descriptor
+  for (int f = 0; f < 8; ++f)
+    for (int64_t v : kI64) {
+      ssd_desc_t d = valid_base();
+      int64_t* fields[] = {&d.batch, &d.seqlen, &d.nheads, &d.headdim, &d.ngroups, &d.dstate, &d.chunk, &d.nseq};
+      *fields[f] = v;
+      bad += check(d);
+      d.varlen = 1;
+      d.batch = 1;
+      bad += check(d);
+    }
+  // every edge value in every 32-bit field
+  for (int f = 0; f < 13; ++f)
+    for (int32_t v : kI32) {
+      ssd_desc_t d = valid_base();
+      int32_t* fields[] = {&d.dtype, &d.state_dtype, &d.a_mode, &d.has_dt, &d.has_D, &d.has_z, &d.has_init,
+                           &d.has_dfinal, &d.varlen, &d.want_final, &d.want_A_cumsum, &d.dA_skip, &d.trapz};
+      *fields[f] = v;
+      bad += check(d);
+    }
+  // seeded random mixtures
+  for (int it = 0; it < 200000 && bad < 10; ++it) {
+    ssd_desc_t d = valid_base();
+    const uint64_t m = next_u64();
+    if (m & (1u << 0)) d.batch = pick(kI64);
+    if (m & (1u << 1)) d.seqlen = pick(kI64);
+    if (m & (1u << 2)) d.nheads = pick(kI64);
+    if (m & (1u << 3)) d.headdim = pick(kI64);
+    if (m & (1u << 4)) d.ngroups = pick(kI64);
+    if (m & (1u << 5)) d.dstate = pick(kI64);
+    if (m & (1u << 6)) d.chunk = pick(kI64);
+    if (m & (1u << 7)) d.nseq = pick(kI64);
+    if (m & (1u << 8)) d.dtype = pick(kI32);
+    if (m & (1u << 9)) d.state_dtype = pick(kI32);
+    if (m & (1u << 10)) d.a_mode = pick(kI32);
+    if (m & (1u << 11)) d.has_dt = pick(kI32);
+    if (m & (1u << 12)) d.has_z = pick(kI32);
+    if (m & (1u << 13)) d.has_init = pick(kI32);
+    if (m & (1u << 14)) d.varlen = pick(kI32);
+    if (m & (1u << 15)) d.want_A_cumsum = pick(kI32);
+    if (m & (1u << 16)) d.dA_skip = pick(kI32);
+    if (m & (1u << 17)) d.trapz = pick(kI32);
+    if (m & (1u << 18)) d.norm_eps = pick(kF32);
+    if (m & (1u << 19)) d.want_final = pick(kI32);
+    if (m & (1u << 20)) d.has_dfinal = pick(kI32);
+    bad += check(d);
+  }
+  std::printf("validate_fuzz: %s\n", bad ? "FAILED" : "ok");
+  return bad ? 1 : 0;
+}
