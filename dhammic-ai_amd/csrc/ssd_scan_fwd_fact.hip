@@ -60,7 +60,9 @@ struct FactStage {
   float cs, dt;
 };
 
-// Row-major staged tile to LDS with every row r scaled by sc[r] (fp32) before rounding.
+// Row-major staged tile to LDS with every row r scaled by sc[r] (fp32) before rounding, into an
+// unpadded W-wide tile with granule-permuted rows (swz_tr: its transposed reads hit distinct banks,
+// where the padded pitch put rows r and r + 2 of a read on the same ones).
 template <int ROWS, int W, int NTHR>
 __device__ __forceinline__ void tstage_store_scaled(const TileStage<ROWS, W, NTHR>& s, bf16* t,
                                                     const float* __restrict__ sc) {
@@ -74,7 +76,7 @@ __device__ __forceinline__ void tstage_store_scaled(const TileStage<ROWS, W, NTH
       bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)s.v[q][e] * f);
-      *reinterpret_cast<bf16x8*>(t + toff<W>(r, k)) = o;
+      *reinterpret_cast<bf16x8*>(t + r * W + (swz_tr<W>(r, k >> 3) << 3)) = o;
     }
   }
 }
@@ -286,7 +288,7 @@ __device__ __forceinline__ void fact_body(const FactCtx<PT, NT, NB>& a, unsigned
         }
         const bf16* xj = xt + j * XT;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) mfma(acc, ttr_perm<PP>(xj, 32 * sh, kk, 32 * pt, lane), S[u][kk]);
+        for (int kk = 0; kk < 2; ++kk) mfma(acc, swz_tr_perm<PP>(xj, 32 * sh, kk, 32 * pt, lane), S[u][kk]);
       }
       // acc * exp(cs_l - c_i) + exp(clamp(cs_l)) h_in C^T: scale by exp(cs_l - c_i) / e_off,
       // accumulate h_in C^T, scale by e_off in the epilogue

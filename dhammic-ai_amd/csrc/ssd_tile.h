@@ -289,6 +289,13 @@ __device__ __forceinline__ bf16x8 swz_tr8(const bf16* t, int k0, int mbase, int 
   const int m0 = mbase + (((L >> 4) & 1) << 4);
   return cat8(swz_tr4<W>(t, k0 + 8 * h, m0, L), swz_tr4<W>(t, k0 + 8 * h + 4, m0, L));
 }
+// The ttr_perm operand order (rows k0 + 16 kk + 4 (L / 32) + 0..3, then + 8) from a permuted tile.
+template <int W>
+__device__ __forceinline__ bf16x8 swz_tr_perm(const bf16* t, int k0, int kk, int mbase, int L) {
+  const int h = L >> 5;
+  const int m0 = mbase + (((L >> 4) & 1) << 4);
+  return cat8(swz_tr4<W>(t, k0 + 16 * kk + 4 * h, m0, L), swz_tr4<W>(t, k0 + 16 * kk + 8 + 4 * h, m0, L));
+}
 // The same for the 16 x 16 x 32 MFMA operand layout: i = mbase + L % 16, k = k0 + 8 (L / 16) + 0..7.
 template <int W>
 __device__ __forceinline__ bf16x8 swz_tr8_16(const bf16* t, int k0, int mbase, int L) {
