@@ -263,9 +263,12 @@ __device__ __forceinline__ void tstage_load_f32(TileStage<ROWS, W, NTHR>& s, con
 // is for the 16 x 16 x 32 operand, whose 16-lane groups read rows k .. k + 3
 // and k + 8 .. k + 11 in one half-wave: without it the two groups hit the same
 // banks (a 32-wide read keeps bit 3 fixed over a half-wave and is unaffected).
+// 128-wide rows (256 bytes) all start in the same bank window, so there the four
+// rows of a read take a quarter of the row each ((r & 3) << 2), bit 3 again
+// moving the second 16-lane group's rows to the other granules of their quarter.
 template <int W>
 __device__ __forceinline__ int swz_tr(int r, int g) {
-  return W >= 64 ? g ^ ((r & 3) << 1) ^ ((r >> 2) & 2) : g;
+  return W == 128 ? g ^ ((r & 3) << 2) ^ ((r >> 2) & 2) : (W >= 64 ? g ^ ((r & 3) << 1) ^ ((r >> 2) & 2) : g);
 }
 // Tiles read by rows (16 consecutive rows at one granule):
 template <int W>
