@@ -12,13 +12,14 @@
 // and dinit = run. The running state stays in the MFMA accumulator registers;
 // nothing but hin / dst (bf16) and the final / initial state is written.
 //
-// One block per (pair of 32-wide n tiles, head, sequence) with 2 PT waves. In the
-// forward walk with head dims 33..64 (PT = 2) wave w owns all 64 rows p of the 16
-// columns 16 w .. 16 w + 15 of the pair (four 16 x 16 MFMA tiles), so each B element
-// is scaled by the per-token factor once per block; otherwise wave w owns the
-// 32 x 32 tile (p tile w % PT, n tile w / PT). Blocks of one (head, sequence) are numbered
-// onto one XCD (same block index mod 8) so their shared x / dy rows come from
-// HBM once. Tokens go 64 at a time through a ring of three LDS slots filled by
+// One block per (head, sequence) over all Npad = 32 NT state columns, with PT NT waves:
+// the walk is bound by its DMA stream (without the B / C columns it runs in 79 % of
+// the time, without the x / dy rows in 73 %), so each x / dy row is loaded once per
+// head, not once per group of columns. In the forward walk with head dims 33..64
+// (PT = 2) wave w owns all 64 rows p of the 16 columns 16 w .. 16 w + 15 (four 16 x 16
+// MFMA tiles), so each B element is scaled by the per-token factor once per block;
+// otherwise wave w owns the 32 x 32 tile (p tile w % PT, n tile w / PT). Tokens go 64
+// at a time through a ring of three LDS slots filled by
 // buffer_load ... lds (x or dy rows, the pair's B or C columns, and the tokens'
 // precomputed factors exp(clamp(cs_last - cs_t)) dt_t or exp(clamp(cs_t))),
 // issued two steps ahead with explicit vmcnt waits, so no register holds
@@ -31,27 +32,32 @@
 
 namespace {
 
-template <int PT>
+template <int PT, int NT>
 struct StateCfg {
   static constexpr int PP = 32 * PT;            // state rows per block
-  static constexpr int NW = 2 * PT;             // waves: (p tile, n tile of the pair)
+  static constexpr int NC = 32 * NT;            // state columns per block (all of Npad)
+  static constexpr int NW = PT * NT;            // waves: (p tile, n tile)
   static constexpr int NTHR = 64 * NW;
   static constexpr int R = 3;                   // ring slots
   static constexpr int UB = 64 * PP * 2;        // x / dy rows of a step
-  static constexpr int VB = 64 * 64 * 2;        // B / C rows of a step, the pair's 64 columns
-  static constexpr int SLOT = UB + VB + NW * 256;  // + one 64-float row per wave (wave 0: the factors)
+  static constexpr int VB = 64 * NC * 2;        // B / C rows of a step
+  static constexpr int SLOT = UB + VB + 256;    // + the step's 64 per-token factors (loaded by wave 0)
   static constexpr int UI = UB / 1024, VI = VB / 1024;  // 1 KB DMA instructions
   static constexpr int PERW = (UI + VI) / NW;   // row DMAs per wave and step
-  static constexpr int D = PERW + 1;            // DMAs per wave and step (+ one scalar row)
+  static constexpr int D = PERW, D0 = PERW + 1; // DMAs per step: any wave, wave 0 (+ the factor row)
   static_assert((UI + VI) % NW == 0, "DMA split");
   static constexpr int TP = 40;                 // s_tile row pitch (elements), 32 x 32 tiles
   // PT = 2: each wave owns all 64 p of 16 columns of the pair (four 16 x 16 MFMA tiles), so every
   // B / C element is scaled by one wave, not by both p-tile waves; other PT use 32 x 32 tiles
   static constexpr int TW = 24;                 // s_tile row pitch (elements), 64 x 16 tiles
   static constexpr int TWE = PT == 2 ? 64 * TW : 32 * TP;  // s_tile elements per wave
-  static size_t bytes(bool bwd) {
-    return (size_t)R * SLOT + NW * TWE * 2 + (bwd ? NW * 2048 : 0);
-  }
+  // The backward walk's h_in tile of a chunk (2 KB per wave) shares the wave's state tile: the tile is
+  // written and read at the chunk's first step before the h_in DMAs are issued into it, which are read
+  // at the chunk's end, before the next chunk's first step.
+  static constexpr int TILE = TWE * 2 > 2048 ? TWE * 2 : 2048;  // bytes per wave
+  static size_t bytes(bool) { return (size_t)R * SLOT + (size_t)NW * TILE; }
+  // waves per SIMD the LDS allows (one block of 16 waves at P = N = 128, else two per SIMD)
+  static constexpr int WPE = NW >= 16 ? 4 : 2;
 };
 
 // Whether the walk uses the 64 x 16 wave tiles: the forward walk at PT = 2. The backward walk
@@ -85,7 +91,7 @@ struct StateCtx {
   const bf16* hin_in;
   float* dtot_part;
   int64_t urow, vrow, ucol, vcol;
-  int h, np, w, pt, ntl, nt, NTn, c0, c1, nch;
+  int h, w, pt, ntl, nt, NTn, c0, c1, nch;
   int ncol0;  // first state column (n) of this wave's tile
   bool nt_ok;
 };
@@ -142,23 +148,23 @@ struct IssueCur {
 };
 
 // Per-wave loop invariants of the ring DMAs. Every wave issues UPW row DMAs of x / dy and VPW of
-// B / C per step (the same split in every wave, so no wave branches on its share), plus one
-// scalar row: wave 0 cs, wave 1 dt (forward, when given), the others a masked one.
-template <int PT>
+// B / C per step (the same split in every wave, so no wave branches on its share); wave 0 also the
+// step's row of per-token factors.
+template <int PT, int NT>
 struct IssueLanes {
-  using Cfg = StateCfg<PT>;
+  using Cfg = StateCfg<PT, NT>;
   static constexpr int UPW = Cfg::UI / Cfg::NW, VPW = Cfg::VI / Cfg::NW;
   static_assert(Cfg::UI % Cfg::NW == 0 && Cfg::VI % Cfg::NW == 0, "per-wave DMA split");
   int ou[UPW], ov[VPW];  // lane's byte offset within the step's rows (SSD_BUF_SIZE: column outside)
   int lu[UPW], lv[VPW];  // lane's row within the step
-  int os;                // factor row: lane's byte offset (SSD_BUF_SIZE: this wave loads none)
 };
 
-template <int PT, bool FWD>
-__device__ __forceinline__ IssueLanes<PT> issue_lanes(const StateCtx& x, int lane) {
-  using Cfg = StateCfg<PT>;
-  using IL = IssueLanes<PT>;
+template <int PT, int NT, bool FWD>
+__device__ __forceinline__ IssueLanes<PT, NT> issue_lanes(const StateCtx& x, int lane) {
+  using Cfg = StateCfg<PT, NT>;
+  using IL = IssueLanes<PT, NT>;
   constexpr int PP = Cfg::PP, UG = PP / 8, URI = 64 / UG;  // granules per U row, U rows per DMA
+  constexpr int NC = Cfg::NC, VG = NC / 8, VRI = 64 / VG;  // ... and per V row
   const SsdDims& d = x.d;
   IL il;
 #pragma unroll
@@ -171,18 +177,17 @@ __device__ __forceinline__ IssueLanes<PT> issue_lanes(const StateCtx& x, int lan
 #pragma unroll
   for (int q = 0; q < IL::VPW; ++q) {
     const int vi = x.w * IL::VPW + q;
-    const int r = vi * 8 + lane / 8, gcol = swz_tr<64>(r, lane % 8) << 3;
+    const int r = vi * VRI + lane / VG, gcol = swz_tr<NC>(r, lane % VG) << 3;
     il.lv[q] = r;
-    il.ov[q] = 64 * x.np + gcol < d.N ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE;
+    il.ov[q] = gcol < d.N ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE;
   }
-  il.os = x.w == 0 ? lane * 4 : SSD_BUF_SIZE;
   return il;
 }
 
 // Enter the issue cursor's chunk u.k (its table entry is u.nci, or loaded here at the first
 // chunk): the bases of its rows, and the next chunk's entry.
-template <int PT, bool FWD>
-__device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<PT>& il, IssueCur& u, bool first) {
+template <int PT, int NT, bool FWD>
+__device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<PT, NT>& il, IssueCur& u, bool first) {
   const SsdDims& d = x.d;
   const int c = walk_chunk<FWD>(x, u.k);
   u.ci = first ? x.chunks[c] : u.nci;
@@ -192,14 +197,14 @@ __device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<
   u.bs = x.fac + ((int64_t)c * d.H + x.h) * d.Qpad;
 }
 
-// One step's DMAs into ring slot `nxt`: StateCfg::D per wave, also past the last step
-// (then masked to zeros), so that every step issues the same count. Advances the
+// One step's DMAs into ring slot `nxt`: StateCfg::D per wave (D0 in wave 0), also past the
+// last step (then masked to zeros), so that every step issues the same count. Advances the
 // issue cursor.
-template <int PT, bool FWD>
-__device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<PT>& il, unsigned char* __restrict__ nxt,
+template <int PT, int NT, bool FWD>
+__device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<PT, NT>& il, unsigned char* __restrict__ nxt,
                                             IssueCur& u, int lane) {
-  using Cfg = StateCfg<PT>;
-  using IL = IssueLanes<PT>;
+  using Cfg = StateCfg<PT, NT>;
+  using IL = IssueLanes<PT, NT>;
   const bool live = u.k < x.nch;
   const int t0i = live ? u.t : 0;
   const int nrows = live ? min(64, u.ci.len - t0i) : 0;
@@ -219,17 +224,37 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rv, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + (x.w * IL::VPW + q) * 1024), 16, vo, sv, 0, 0);
   }
-  {
-    const int vo = il.os, so = t0i * 4;
+  if (x.w == 0) {
+    const int vo = lane * 4, so = t0i * 4;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB + x.w * 256), 4, vo, so, 0, 0);
+        rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB), 4, vo, so, 0, 0);
   }
   if (live) {
     u.t += 64;
     if (u.t >= u.ci.len) {
       ++u.k;
       u.t = 0;
-      issue_fetch<PT, FWD>(x, il, u, false);
+      issue_fetch<PT, NT, FWD>(x, il, u, false);
+    }
+  }
+}
+
+// vmcnt wait until at most n steps' ring DMAs of this wave are outstanding (n <= 3)
+template <int D0, int D>
+__device__ __forceinline__ void wait_ring(int w, int n) {
+  if (w == 0) {
+    switch (n) {
+      case 0: wait_vm<0>(); break;
+      case 1: wait_vm<D0>(); break;
+      case 2: wait_vm<2 * D0>(); break;
+      default: wait_vm<3 * D0>(); break;
+    }
+  } else {
+    switch (n) {
+      case 0: wait_vm<0>(); break;
+      case 1: wait_vm<D>(); break;
+      case 2: wait_vm<2 * D>(); break;
+      default: wait_vm<3 * D>(); break;
     }
   }
 }
@@ -238,18 +263,17 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
 // step goes through these distinct __restrict__ pointers, which tells the compiler
 // that the new DMAs do not write what the step reads: it then adds no wait of its
 // own for them, and the slot waits stay the explicit ones of the caller.
-template <int PT, bool FWD>
+template <int PT, int NT, bool FWD>
 __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
-                                           unsigned char* __restrict__ nxt,
-                                           bf16* __restrict__ tw, bf16* __restrict__ hbw,
-                                           const IssueLanes<PT>& il, IssueCur& ui, Cursor& uc, int& st,
+                                           unsigned char* __restrict__ nxt, bf16* __restrict__ tw,
+                                           const IssueLanes<PT, NT>& il, IssueCur& ui, Cursor& uc, int& st,
                                            int& s_start, floatx16& acc, floatx16& run) {
-  using Cfg = StateCfg<PT>;
+  using Cfg = StateCfg<PT, NT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
   constexpr bool WIDE = state_wide<PT, FWD>();
   const SsdDims& d = x.d;
   const int lane = threadIdx.x & 63;
-  state_issue<PT, FWD>(x, il, nxt, ui, lane);
+  state_issue<PT, NT, FWD>(x, il, nxt, ui, lane);
   const int c = uc.c;
   const int clen = uc.ci.len;
   int& t0 = uc.t;
@@ -281,7 +305,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
       for (int q = 0; q < 2; ++q) {
         const int r = (TR / 2) * q + lane / GPR, c8 = (lane % GPR) * 8;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rh, (__attribute__((address_space(3))) void*)(hbw + q * 512), 16,
+            rh, (__attribute__((address_space(3))) void*)(tw + q * 512), 16,
             x.nt_ok ? (int)(((prow0 + r) * d.Npad + x.ncol0 + c8) * 2) : SSD_BUF_SIZE, 0, 0, 0);
       }
     }
@@ -297,7 +321,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
     for (int kk = 0; kk < 64; kk += 32) {
       const floatx4 f0 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 4));
       const floatx4 f1 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 4) + 4);
-      bf16x8 b = swz_tr8_16<64>(tv, kk, 16 * x.w, lane);
+      bf16x8 b = swz_tr8_16<Cfg::NC>(tv, kk, 16 * x.w, lane);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         b[e] = (bf16)((float)b[e] * f0[e]);
@@ -313,7 +337,7 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
     for (int kk = 0; kk < 64; kk += 16) {
       const floatx4 f0 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 5));
       const floatx4 f1 = *reinterpret_cast<const floatx4*>(fac + kk + 8 * (lane >> 5) + 4);
-      bf16x8 b = swz_tr8<64>(tv, kk, 32 * x.ntl, lane);
+      bf16x8 b = swz_tr8<Cfg::NC>(tv, kk, 32 * x.ntl, lane);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         b[e] = (bf16)((float)b[e] * f0[e]);
@@ -331,15 +355,10 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
     if (!FWD) {
       // the h_in tile's DMAs were issued at the chunk's first step, before the ring DMAs
       // of the (st - 1 - s_start) steps since
-      switch (st - 1 - s_start) {
-        case 0: wait_vm<0>(); break;
-        case 1: wait_vm<Cfg::D>(); break;
-        case 2: wait_vm<2 * Cfg::D>(); break;
-        default: wait_vm<3 * Cfg::D>(); break;
-      }
+      wait_ring<Cfg::D0, Cfg::D>(x.w, st - 1 - s_start);
       float contrib = 0.0f;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) contrib += run[v] * (float)hbw[state_row<WIDE>(v, lane) * TC + state_col<WIDE>(lane)];
+      for (int v = 0; v < 16; ++v) contrib += run[v] * (float)tw[state_row<WIDE>(v, lane) * TC + state_col<WIDE>(lane)];
       contrib *= dec * clamp_pass(tot);
       contrib = wave_sum(contrib);
       // one partial per wave, (32-wide n tile, p tile or 16-wide half) in order: no block
@@ -356,43 +375,41 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
   }
 }
 
-// LDS allows two waves per SIMD at every PT (two blocks of 2 PT waves up to PT = 2, one of 8 at PT = 4)
-template <int PT, bool FWD>
-__global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2, 2))) k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
+// LDS allows StateCfg::WPE waves per SIMD (two, or four for the 16-wave block at P = N = 128)
+template <int PT, int NT, bool FWD>
+__global__ void __launch_bounds__(64 * PT * NT) __attribute__((amdgpu_waves_per_eu(StateCfg<PT, NT>::WPE, StateCfg<PT, NT>::WPE)))
+k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
                                                          const float* __restrict__ cs, const float* __restrict__ fac,
                                                          const bf16* __restrict__ U, const bf16* __restrict__ V,
                                                          bf16* __restrict__ hst, const bf16* __restrict__ hin_in,
                                                          const void* __restrict__ s_in, void* __restrict__ s_out,
                                                          int state_bf16, float* __restrict__ dtot_part) {
-  using Cfg = StateCfg<PT>;
+  using Cfg = StateCfg<PT, NT>;
   constexpr int TP = Cfg::TP, SLOT = Cfg::SLOT;
   constexpr bool WIDE = state_wide<PT, FWD>();
   extern __shared__ __align__(16) unsigned char smem[];
-  bf16* s_tile = reinterpret_cast<bf16*>(smem + Cfg::R * SLOT);          // [NW][TWE] state tiles
-  bf16* hb = s_tile + Cfg::NW * Cfg::TWE;                                 // [NW][1024] (backward: h_in)
+  // [NW][TILE bytes]: each wave's state tile, and in the backward walk its h_in tile
+  unsigned char* s_tile = smem + Cfg::R * SLOT;
 
-  // block -> (n tile pair, unit = (head, sequence)); the pairs of a unit share an XCD
+  // block -> unit = (head, sequence)
   StateCtx x;
   x.d = d;
   x.NTn = d.Npad / 32;
-  const int NPR = (x.NTn + 1) / 2;
-  const int x8 = blockIdx.x & 7, rr = blockIdx.x >> 3;
-  x.np = rr % NPR;
-  const int unit = (rr / NPR) * 8 + x8;
+  const int unit = blockIdx.x;
   if (unit >= d.H * d.nseq) return;
   x.h = unit % d.H;
   const int sq = unit / d.H;
   const int g = x.h / d.hpg;
   x.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if constexpr (WIDE) {  // wave w: all p, columns 16 w .. 16 w + 15 of the pair
+  if constexpr (WIDE) {  // wave w: all p, columns 16 w .. 16 w + 15
     x.pt = 0;
     x.ntl = x.w >> 1;
-    x.ncol0 = 64 * x.np + 16 * x.w;
-  } else {                    // wave w: p tile w % PT, 32-wide column tile w / PT of the pair
+    x.ncol0 = 16 * x.w;
+  } else {                    // wave w: p tile w % PT, 32-wide column tile w / PT
     x.pt = x.w % PT;
     x.ntl = x.w / PT;
-    x.ncol0 = 64 * x.np + 32 * x.ntl;
+    x.ncol0 = 32 * x.ntl;
   }
   x.nt = x.ncol0 / 32;
   x.nt_ok = x.nt < x.NTn;
@@ -407,7 +424,7 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   x.urow = (int64_t)d.H * d.P;
   x.vrow = (int64_t)d.G * d.N;
   x.ucol = (int64_t)x.h * d.P;
-  x.vcol = (int64_t)g * d.N + 64 * x.np;
+  x.vcol = (int64_t)g * d.N;
   const int lane = threadIdx.x & 63;
   const int n = x.ncol0 + state_col<WIDE>(lane);
   const int prow0 = 32 * x.pt;
@@ -430,14 +447,14 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   x.c1 = seq_chunk0[sq + 1];
   x.nch = x.c1 - x.c0;
 
-  const IssueLanes<PT> il = issue_lanes<PT, FWD>(x, lane);
+  const IssueLanes<PT, NT> il = issue_lanes<PT, NT, FWD>(x, lane);
   IssueCur ui{};                  // issue cursor
   Cursor uc{};                    // compute cursor
   if (x.nch > 0) {  // (an empty sequence passes its state through)
-    issue_fetch<PT, FWD>(x, il, ui, true);
+    issue_fetch<PT, NT, FWD>(x, il, ui, true);
     cursor_init<FWD>(x, uc);
-    state_issue<PT, FWD>(x, il, smem, ui, lane);
-    state_issue<PT, FWD>(x, il, smem + SLOT, ui, lane);
+    state_issue<PT, NT, FWD>(x, il, smem, ui, lane);
+    state_issue<PT, NT, FWD>(x, il, smem + SLOT, ui, lane);
   }
   floatx16 acc;
   zero(acc);
@@ -445,11 +462,11 @@ __global__ void __launch_bounds__(128 * PT) __attribute__((amdgpu_waves_per_eu(2
   // step st reads slot st % 3 and refills slot (st + 2) % 3; unrolled three times so that every
   // slot address is a constant (the LDS reads carry it in their offset field)
   static_assert(Cfg::R == 3, "three-slot ring");
+  bf16* tw = reinterpret_cast<bf16*>(s_tile + x.w * Cfg::TILE);
   auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
-    wait_vm<Cfg::D>();  // this wave's DMAs of slot st are done (the next slot's may still fly)
-    lds_barrier();      // ... and every wave's; step st - 1 is done everywhere, its slot free
-    state_step<PT, FWD>(x, cur, nxt, s_tile + x.w * Cfg::TWE, hb + x.w * 1024, il, ui, uc, st,
-                        s_start, acc, run);
+    wait_ring<Cfg::D0, Cfg::D>(x.w, 1);  // this wave's DMAs of slot st are done (the next slot's may still fly)
+    lds_barrier();  // ... and every wave's; step st - 1 is done everywhere, its slot free
+    state_step<PT, NT, FWD>(x, cur, nxt, tw, il, ui, uc, st, s_start, acc, run);
   };
   while (uc.k < x.nch) {
     step(smem, smem + 2 * SLOT);
@@ -480,16 +497,26 @@ bool state_fused_supported(int dtype, const SsdDims& d) {
 // dtot partials per (chunk, head) of the backward walk: one per wave, i.e. per 32 x 32 tile
 int state_fused_slices(const SsdDims& d) { return d.Npad / 32 * (d.Ppad / 32); }
 
-template <int PT, bool FWD>
+template <int PT, int NT, bool FWD>
 static void state_fused_launch(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* fac,
                                bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
                                hipStream_t s) {
-  const int units = d.H * d.nseq, npr = (d.Npad / 32 + 1) / 2;
-  const dim3 grid((units + 7) / 8 * 8 * npr);
-  const size_t lds = StateCfg<PT>::bytes(!FWD);
-  ensure_lds(k_state_fused<PT, FWD>, lds);
-  hipLaunchKernelGGL((k_state_fused<PT, FWD>), grid, dim3(StateCfg<PT>::NTHR), lds, s, d, b.chunks, b.seq_chunk0,
+  using Cfg = StateCfg<PT, NT>;
+  const dim3 grid(d.H * d.nseq);
+  const size_t lds = Cfg::bytes(!FWD);
+  ensure_lds(k_state_fused<PT, NT, FWD>, lds);
+  hipLaunchKernelGGL((k_state_fused<PT, NT, FWD>), grid, dim3(Cfg::NTHR), lds, s, d, b.chunks, b.seq_chunk0,
                      b.cs, fac, u, v, hst, hin_in, s_in, s_out, state_bf16, b.dtot_part);
+}
+template <int PT, bool FWD>
+static void state_fused_nt(const SsdDims& d, const SsdBufs& b, const bf16* u, const bf16* v, const float* fac,
+                           bf16* hst, const bf16* hin_in, const void* s_in, void* s_out, int state_bf16,
+                           hipStream_t s) {
+  switch (d.Npad / 32) {
+    case 1: state_fused_launch<PT, 1, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    case 2: state_fused_launch<PT, 2, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    default: state_fused_launch<PT, 4, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s);
+  }
 }
 
 template <bool FWD>
@@ -499,9 +526,9 @@ static hipError_t state_fused_t(const SsdDims& d, const SsdBufs& b, const void* 
   const bf16* u = reinterpret_cast<const bf16*>(U);
   const bf16* v = reinterpret_cast<const bf16*>(V);
   switch (d.Ppad / 32) {
-    case 1: state_fused_launch<1, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
-    case 2: state_fused_launch<2, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
-    default: state_fused_launch<4, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s);
+    case 1: state_fused_nt<1, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    case 2: state_fused_nt<2, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s); break;
+    default: state_fused_nt<4, FWD>(d, b, u, v, fac, hst, hin_in, s_in, s_out, state_bf16, s);
   }
   return hipGetLastError();
 }
