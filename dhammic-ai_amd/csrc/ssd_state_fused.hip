@@ -38,7 +38,7 @@ struct StateCfg {
   static constexpr int NC = 32 * NT;            // state columns per block (all of Npad)
   static constexpr int NW = PT * NT;            // waves: (p tile, n tile)
   static constexpr int NTHR = 64 * NW;
-  static constexpr int R = 3;                   // ring slots
+  static constexpr int R = (PT == 2 && NT == 4) ? 4 : 3;  // ring slots
   static constexpr int UB = 64 * PP * 2;        // x / dy rows of a step
   static constexpr int VB = 64 * NC * 2;        // B / C rows of a step
   static constexpr int SLOT = UB + VB + 256;    // + the step's 64 per-token factors (loaded by wave 0)
@@ -453,27 +453,39 @@ k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
   if (x.nch > 0) {  // (an empty sequence passes its state through)
     issue_fetch<PT, NT, FWD>(x, il, ui, true);
     cursor_init<FWD>(x, uc);
-    state_issue<PT, NT, FWD>(x, il, smem, ui, lane);
-    state_issue<PT, NT, FWD>(x, il, smem + SLOT, ui, lane);
+    for (int q = 0; q < Cfg::R - 1; ++q) state_issue<PT, NT, FWD>(x, il, smem + q * SLOT, ui, lane);
   }
   floatx16 acc;
   zero(acc);
   int st = 0, s_start = 0;  // step count, step of the chunk's start
-  // step st reads slot st % 3 and refills slot (st + 2) % 3; unrolled three times so that every
+  // step st reads slot st % R and refills slot (st + R - 1) % R; unrolled R times so that every
   // slot address is a constant (the LDS reads carry it in their offset field)
-  static_assert(Cfg::R == 3, "three-slot ring");
+  static_assert(Cfg::R == 3 || Cfg::R == 4, "three- or four-slot ring");
   bf16* tw = reinterpret_cast<bf16*>(s_tile + x.w * Cfg::TILE);
   auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
-    wait_ring<Cfg::D0, Cfg::D>(x.w, 1);  // this wave's DMAs of slot st are done (the next slot's may still fly)
+    // this wave's DMAs of slot st are done (those of the next R - 2 slots may still fly)
+    wait_ring<Cfg::D0, Cfg::D>(x.w, Cfg::R - 2);
     lds_barrier();  // ... and every wave's; step st - 1 is done everywhere, its slot free
     state_step<PT, NT, FWD>(x, cur, nxt, tw, il, ui, uc, st, s_start, acc, run);
   };
-  while (uc.k < x.nch) {
-    step(smem, smem + 2 * SLOT);
-    if (uc.k >= x.nch) break;
-    step(smem + SLOT, smem);
-    if (uc.k >= x.nch) break;
-    step(smem + 2 * SLOT, smem + SLOT);
+  if constexpr (Cfg::R == 4) {
+    while (uc.k < x.nch) {
+      step(smem, smem + 3 * SLOT);
+      if (uc.k >= x.nch) break;
+      step(smem + SLOT, smem);
+      if (uc.k >= x.nch) break;
+      step(smem + 2 * SLOT, smem + SLOT);
+      if (uc.k >= x.nch) break;
+      step(smem + 3 * SLOT, smem + 2 * SLOT);
+    }
+  } else {
+    while (uc.k < x.nch) {
+      step(smem, smem + 2 * SLOT);
+      if (uc.k >= x.nch) break;
+      step(smem + SLOT, smem);
+      if (uc.k >= x.nch) break;
+      step(smem + 2 * SLOT, smem + SLOT);
+    }
   }
   wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
   // final state (forward) / gradient of the initial state (backward)
