@@ -76,25 +76,59 @@ hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t*
 // coefficient kernel writes the chunk's positions with its own dt), ffac2
 // (trapezoidal gamma walk: zeros here likewise).
 // ---------------------------------------------------------------------------
+// One row of Qpad fp32 values, `per` consecutive positions per lane: a 16-byte store per lane when
+// each lane holds four and the row is 16-byte aligned.
+__device__ __forceinline__ void store_row(float* __restrict__ p, int lane, int per, const float (&v)[4]) {
+  if (per == 4 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    *reinterpret_cast<float4*>(p + lane * 4) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    for (int e = 0; e < per; ++e) p[lane * per + e] = v[e];
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                       const void* __restrict__ Av, const float* __restrict__ dt,
                                                       float* __restrict__ cs, T* __restrict__ acs_out,
                                                       int32_t* __restrict__ fast, float* __restrict__ ffac,
                                                       float* __restrict__ ffac2, float* __restrict__ bfac) {
+  // dt of the block's four heads, [head][position] (Qpad <= 256)
+  __shared__ float s_dt[4][256];
   const int c = blockIdx.x;
-  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int h0 = blockIdx.y * 4, hw = threadIdx.x >> 6;
+  const int h = h0 + hw;
   const int lane = lane_id();
-  if (h >= d.H) return;
   const ChunkInfo ci = chunks[c];
-  if (ci.len == 0) return;
-  const int per = d.Qpad / 64;  // 1, 2 or 4 consecutive positions per lane
-  float v[4], dtv[4];
+  if (ci.len == 0) return;  // the whole block
+  const bool use_dt = d.has_dt && !d.trapz;
+  if (use_dt) {
+    // dt is token-major ([R][H]): one thread per position reads the four heads' values, one 16-byte
+    // load when they are in range and aligned, where a lane per head would touch a line per position
+    const int l = threadIdx.x;
+    if (l < d.Qpad) {
+      float q[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      if (l < ci.len) {
+        const float* p = dt + ((int64_t)ci.row0 + l) * d.H + h0;
+        if ((d.H & 3) == 0 && (reinterpret_cast<uintptr_t>(dt) & 15) == 0) {
+          const float4 f = *reinterpret_cast<const float4*>(p);
+          q[0] = f.x; q[1] = f.y; q[2] = f.z; q[3] = f.w;
+        } else {
+          for (int k = 0; k < 4; ++k)
+            if (h0 + k < d.H) q[k] = p[k];
+        }
+      }
+      for (int k = 0; k < 4; ++k) s_dt[k][l] = q[k];
+    }
+    __syncthreads();
+  }
+  if (h >= d.H) return;
+  const int per = d.Qpad / 64;  // 1 to 4 consecutive positions per lane
+  float v[4] = {}, dtv[4] = {};
   float run = 0.0f;
   for (int e = 0; e < per; ++e) {
     const int l = lane * per + e;
     float a = 0.0f;
-    dtv[e] = (d.has_dt && !d.trapz && l < ci.len) ? dt[(ci.row0 + l) * d.H + h] : 1.0f;
+    dtv[e] = (use_dt && l < ci.len) ? s_dt[hw][l] : 1.0f;
     if (d.a_mode == 2) {
       // the caller's inclusive cumsum: differences are not needed, keep it as is
       const int nch = d.seqlen / d.Q;
@@ -126,18 +160,20 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
     const float excl = incl - run;
     for (int e = 0; e < per; ++e) v[e] += excl;
   }
-  float* out = cs + ((int64_t)c * d.H + h) * d.Qpad;
-  for (int e = 0; e < per; ++e) out[lane * per + e] = v[e];
+  const int64_t o = ((int64_t)c * d.H + h) * d.Qpad;
+  store_row(cs + o, lane, per, v);
   if (ffac) {
-    const int64_t o = ((int64_t)c * d.H + h) * d.Qpad;
     const float tot = __shfl(v[per - 1], 63, 64);  // cs[Qpad - 1], the chunk total
+    float f[4] = {}, g[4] = {};
+    const float zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int e = 0; e < per; ++e) {
-      const int l = lane * per + e;
-      const bool in = l < ci.len;
-      ffac[o + l] = (in && !d.trapz) ? exp_clamp(tot - v[e]) * dtv[e] : 0.0f;
-      if (ffac2) ffac2[o + l] = 0.0f;
-      bfac[o + l] = in ? exp_clamp(v[e]) : 0.0f;
+      const bool in = lane * per + e < ci.len;
+      f[e] = (in && !d.trapz) ? exp_clamp(tot - v[e]) * dtv[e] : 0.0f;
+      g[e] = in ? exp_clamp(v[e]) : 0.0f;
     }
+    store_row(ffac + o, lane, per, f);
+    if (ffac2) store_row(ffac2 + o, lane, per, zero);
+    store_row(bfac + o, lane, per, g);
   }
   if (fast) {
     // Factorised-decay guard: cs non-increasing over the chunk (every a <= 0)
