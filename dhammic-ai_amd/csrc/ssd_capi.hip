@@ -433,9 +433,8 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   if (fused_state) b.npass_blk = state_fused_slices(d);  // dtot partials: one per 32 x 32 state tile
   const void* dY = a->dy;
   if (d.has_z) {
+    // (its weight gradient's partials are reduced by the backward's last launch, with dA / dD)
     SSD_PHASE(tm, SSD_PH_NORM_BWD, launch_gated_norm_bwd(p.dtype, d, b, in, a->dy, a->dz, s));
-    if (a->dnorm_weight)
-      SSD_PHASE(tm, SSD_PH_NORM_DW, launch_reduce_rows((int)p.norm_blocks, d.H * d.P, b.dw_part, a->dnorm_weight, s));
     dY = b.dyp;
   }
   // One backward of the scan for (dd, bb, ii): the state pass (unless skipped: dst is then the one a
@@ -514,7 +513,10 @@ int ssd_bwd(const ssd_desc_t* desc, const ssd_bwd_args_t* a, const void* saved, 
   }
   float* dA_head = d.a_mode == SSD_A_PER_HEAD ? reinterpret_cast<float*>(a->dA) : nullptr;
   float* dD = d.has_D ? a->dD : nullptr;
-  if (dA_head || dD) SSD_PHASE(tm, SSD_PH_BWD_REDUCE_HEADS, launch_reduce_heads(d, b, dA_head, dD, s));
+  float* dw = d.has_z ? a->dnorm_weight : nullptr;
+  if (dA_head || dD || dw)
+    SSD_PHASE(tm, SSD_PH_BWD_REDUCE_HEADS,
+              launch_reduce_tail(d, b, dA_head, dD, (int)p.norm_blocks, d.H * d.P, b.dw_part, dw, s));
   return SSD_OK;
 }
 

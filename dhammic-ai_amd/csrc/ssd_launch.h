@@ -115,6 +115,8 @@ hipError_t launch_trapz_grads(int dtype, const SsdDims& d, const SsdBufs& b, con
 // ssd_reduce.hip
 hipError_t launch_reduce_slices(int dtype, int64_t nelem, int nslices, const float* part, void* out,
                                 hipStream_t s);
-hipError_t launch_reduce_heads(const SsdDims& d, const SsdBufs& b, float* dA_head, float* dD,
-                               hipStream_t s);
+// dA / dD per head and the norm weight's gradient (out = sum of part's nblocks rows of width) in one launch;
+// either side may be absent (dA_head = dD = nullptr, or out = nullptr)
+hipError_t launch_reduce_tail(const SsdDims& d, const SsdBufs& b, float* dA_head, float* dD, int nblocks, int width,
+                              const float* part, float* out, hipStream_t s);
 hipError_t launch_reduce_rows(int nblocks, int width, const float* part, float* out, hipStream_t s);

@@ -130,7 +130,9 @@ typedef struct ssd_desc {
  * caller may pass `events`: an array of 2*SSD_NUM_PHASES hipEvent_t handles
  * (created by the caller); events[2*k] is recorded on the stream right before
  * the launch(es) of phase k and events[2*k+1] right after. Phases that do not
- * run for a descriptor are not recorded. NULL disables recording. */
+ * run for a descriptor are not recorded. NULL disables recording.
+ * SSD_PH_NORM_DW is no longer recorded: the norm weight's gradient is reduced in
+ * the backward's last launch, timed as SSD_PH_BWD_REDUCE_HEADS. */
 enum ssd_phase {
   SSD_PH_CHUNK_TABLE = 0, SSD_PH_CUMSUM = 1, SSD_PH_FWD_STATE = 2, SSD_PH_FWD_PASS = 3,
   SSD_PH_FWD_SCAN = 4, SSD_PH_NORM_FWD = 5,
