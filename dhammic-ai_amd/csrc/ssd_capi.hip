@@ -283,7 +283,8 @@ int fwd_impl(const ssd_desc_t* desc, const ssd_fwd_args_t* a, void* saved, size_
   SsdIn in = {a->x, dt, a->A, a->B, a->C, a->D, a->z, a->norm_weight, a->init, a->cu_seqlens};
   const PhaseTimer tm{a->events, s};
   const bool fused_state = state_fused_supported(p.dtype, d);
-  SSD_PHASE(tm, SSD_PH_CHUNK_TABLE, launch_chunk_table(d, b, a->cu_seqlens, s));
+  // packed sequences: the chunk table from cu_seqlens; fixed-length batches: written by the cumsum launch
+  if (d.varlen) SSD_PHASE(tm, SSD_PH_CHUNK_TABLE, launch_chunk_table(d, b, a->cu_seqlens, s));
   SSD_PHASE(tm, SSD_PH_CUMSUM,
             launch_chunk_cumsum(p.dtype, d, b, a->A, dt, desc->want_A_cumsum ? a->A_cumsum_out : nullptr, s));
   if (d.trapz) {

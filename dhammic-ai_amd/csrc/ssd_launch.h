@@ -22,6 +22,7 @@ struct SsdIn {
 };
 
 // ssd_prep.hip
+// packed sequences (d.varlen) only: a fixed-length batch's table is written by launch_chunk_cumsum
 hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t* cu, hipStream_t s);
 hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, const void* A,
                                const float* dt, void* A_cumsum_out, hipStream_t s);

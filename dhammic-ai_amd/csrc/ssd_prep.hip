@@ -74,7 +74,8 @@ hipError_t launch_chunk_table(const SsdDims& d, const SsdBufs& b, const int32_t*
 // per-token factors (0 past the chunk's length): bfac = exp(clamp(cs_t)),
 // ffac = exp(clamp(cs_last - cs_t)) dt_t (trapezoidal mode: zeros here, the
 // coefficient kernel writes the chunk's positions with its own dt), ffac2
-// (trapezoidal gamma walk: zeros here likewise).
+// (trapezoidal gamma walk: zeros here likewise). For a fixed-length batch it
+// also writes the chunk table (no k_chunk_table launch).
 // ---------------------------------------------------------------------------
 // One row of Qpad fp32 values, `per` consecutive positions per lane: a 16-byte store per lane when
 // each lane holds four and the row is 16-byte aligned.
@@ -87,7 +88,8 @@ __device__ __forceinline__ void store_row(float* __restrict__ p, int lane, int p
 }
 
 template <typename T>
-__global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo* __restrict__ chunks,
+__global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, ChunkInfo* __restrict__ chunks,
+                                                      int32_t* __restrict__ seq_chunk0, int build_table,
                                                       const void* __restrict__ Av, const float* __restrict__ dt,
                                                       float* __restrict__ cs, T* __restrict__ acs_out,
                                                       int32_t* __restrict__ fast, float* __restrict__ ffac,
@@ -98,7 +100,24 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
   const int h0 = blockIdx.y * 4, hw = threadIdx.x >> 6;
   const int h = h0 + hw;
   const int lane = lane_id();
-  const ChunkInfo ci = chunks[c];
+  ChunkInfo ci;
+  if (build_table) {
+    // Fixed-length batch (max_chunks = nseq * nch, every chunk valid): chunk c is chunk c % nch of
+    // sequence c / nch, the entry k_chunk_table writes for it; the blocks of head group 0 write the table.
+    const int nch = (d.seqlen + d.Q - 1) / d.Q;
+    const int sq = c / nch, k = c - sq * nch;
+    ci.row0 = sq * d.seqlen + k * d.Q;
+    ci.len = min(d.Q, d.seqlen - k * d.Q);
+    ci.seq = sq;
+    ci.idx_in_seq = k;
+    if (blockIdx.y == 0) {
+      if (threadIdx.x == 0) chunks[c] = ci;
+      if (c == 0)
+        for (int q = threadIdx.x; q <= d.nseq; q += blockDim.x) seq_chunk0[q] = q * nch;
+    }
+  } else {
+    ci = chunks[c];
+  }
   if (ci.len == 0) return;  // the whole block
   const bool use_dt = d.has_dt && !d.trapz;
   if (use_dt) {
@@ -212,11 +231,12 @@ __global__ void __launch_bounds__(256) k_chunk_cumsum(SsdDims d, const ChunkInfo
 hipError_t launch_chunk_cumsum(int dtype, const SsdDims& d, const SsdBufs& b, const void* A,
                                const float* dt, void* A_cumsum_out, hipStream_t s) {
   dim3 grid(d.max_chunks, (d.H + 3) / 4);
+  const int build = d.varlen ? 0 : 1;  // fixed-length batches: the chunk table is written here
   if (dtype == 1)
-    hipLaunchKernelGGL(k_chunk_cumsum<bf16>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
+    hipLaunchKernelGGL(k_chunk_cumsum<bf16>, grid, dim3(256), 0, s, d, b.chunks, b.seq_chunk0, build, A, dt, b.cs,
                        reinterpret_cast<bf16*>(A_cumsum_out), b.fast, b.fwd_fac, b.fwd_fac2, b.bwd_fac);
   else
-    hipLaunchKernelGGL(k_chunk_cumsum<float>, grid, dim3(256), 0, s, d, b.chunks, A, dt, b.cs,
+    hipLaunchKernelGGL(k_chunk_cumsum<float>, grid, dim3(256), 0, s, d, b.chunks, b.seq_chunk0, build, A, dt, b.cs,
                        reinterpret_cast<float*>(A_cumsum_out), b.fast, b.fwd_fac, b.fwd_fac2, b.bwd_fac);
   return hipGetLastError();
 }

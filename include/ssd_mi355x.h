@@ -131,6 +131,8 @@ typedef struct ssd_desc {
  * (created by the caller); events[2*k] is recorded on the stream right before
  * the launch(es) of phase k and events[2*k+1] right after. Phases that do not
  * run for a descriptor are not recorded. NULL disables recording.
+ * SSD_PH_CHUNK_TABLE is recorded for packed sequences only (a fixed-length
+ * batch's table is written by the SSD_PH_CUMSUM launch).
  * SSD_PH_NORM_DW is no longer recorded: the norm weight's gradient is reduced in
  * the backward's last launch, timed as SSD_PH_BWD_REDUCE_HEADS. */
 enum ssd_phase {
