@@ -30,9 +30,10 @@
 // (s half w % 2, l half (w / 2) % 2) of the tiles (j + t, j) with t = w / 4 + 2 u
 // for dS, rowG and colG (S^T of those two tiles kept in fp32 registers, built
 // once per block), waves 8-11 own dX^T tile (p tile (w / 2) % 2, s half w % 2)
-// over all l and finish the head's tokens. S^T is staged once per block, in
-// bf16, for the dX waves, which scale it by f_l as they read it; every dy row is
-// staged once, unscaled, for both roles. Each role runs its own copy of the head
+// over all l and finish the head's tokens. While a head is staged, the dS waves
+// write its S'^T = f_l S^T in bf16 from their fp32 quadrants (a lane's quadrant
+// column is one row l, so one factor per lane and tile), and the dX waves read it
+// as their operand; every dy row is staged once, unscaled, for both roles. Each role runs its own copy of the head
 // loop (two barriers per head) and loads part of the next head into registers
 // while a head computes: the dX waves the x rows and the per-token scalars
 // (before their contraction), the dS waves the dy rows and dst (after theirs,
@@ -79,8 +80,8 @@ struct BwdFactLds {
   // one head's per-token reductions: red_e [2 pt][64], red_x [2 pt][64], red_d [4] (64 reserved),
   // red_row [kSlots][2 wr][64], red_col [kSetW][2 wc][64]
   static constexpr int PB = 320 + 128 * kSlots + 128 * kSetW;
-  static constexpr int RED = 2 * PB + 64 + 256;  // by head parity; + v_s and f_l rows of the current head
-  // bf16: xu, ot[2], dyr[4], St[4], dstT, Bt; fp32: reductions and the row factors
+  static constexpr int RED = 2 * PB + 64;  // by head parity; + the v_s row of the current head
+  // bf16: xu, ot[2], dyr[4], St[4], dstT, Bt; fp32: reductions and the column factors
   static size_t bytes(int) { return 2 * (size_t)((3 + kSlots) * XT + kSlots * SQ + DT + BT) + 4 * (size_t)RED; }
 };
 
@@ -142,25 +143,19 @@ __device__ __forceinline__ void ur_set(u32x4* R, const floatx16& f) {
     for (int e = 0; e < 4; ++e) R[q][e] = __float_as_uint(f[4 * q + e]);
 }
 
-// Eight bf16 values times eight fp32 factors f[0..7] (16-byte aligned in LDS), rounded to bf16.
-__device__ __forceinline__ bf16x8 scale8(const bf16x8 v, const float* f) {
-  const floatx4 a = *reinterpret_cast<const floatx4*>(f);
-  const floatx4 b = *reinterpret_cast<const floatx4*>(f + 4);
-  bf16x8 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    o[e] = (bf16)((float)v[e] * a[e]);
-    o[e + 4] = (bf16)((float)v[e + 4] * b[e]);
-  }
-  return o;
-}
-
 // Per-head scalars loaded with the next head's tiles (dX waves).
 struct BwdFactScalars {
-  float fcs;        // cs at row 64 j + (staging thread index): the head's f_l
   float ecs, edt;   // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
   float cj, cl;     // cs at the last token of block j and of the chunk
   float D;          // the head's D (0 without D); trapezoidal mode: D at that token
+  int fast;
+};
+
+// Per-head scalars loaded with the next head's dy rows (dS waves): the f_l of the lane's quadrant
+// row l = 64 (j + t) + 32 wc + lane % 32 of each of its tiles t.
+struct BwdFactRowScalars {
+  float fcs[kNsw];  // cs at those rows
+  float cj;         // cs at the last token of block j
   int fast;
 };
 
@@ -220,7 +215,6 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     return HeadBuf{r, r + 128, r + 256, r + 320, r + 320 + 128 * kSlots, ot2 + (k & 1) * XT};
   };
   float* vrow = red + 2 * LD::PB;  // [64] v_s = dt_s g_s of the current head (0 for a flagged head)
-  float* frow = vrow + 64;         // [256] f_l = exp(cs_l - c_j) at rows 64 j + l of the current head
 
   // ---- B rows of block j; the dS waves' S^T quadrants of tiles (j + t, j), t = ws + kSetW u: rows s
   // (block j), columns l (block j + t), kept in fp32 registers for every head ----
@@ -259,7 +253,8 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         }
       }
       ur_set(UR + 4 * uu, Sq);  // dS (entries 4 (kNsw + u) ..) starts at zero
-      // bf16 copy of S^T[s][l] for the dX waves (also for tiles and quadrants that stay zero)
+      // bf16 copy of S^T[s][l] for the dX waves: quadrants that stay zero keep it, the others are
+      // rewritten as S'^T for each head
       if (t < kSlots) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)Sq[v];
@@ -278,7 +273,8 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   u32x4 YR[nYR];
 #pragma unroll
   for (int q = 0; q < nYR; ++q) YR[q] = u32x4{0u, 0u, 0u, 0u};
-  BwdFactScalars hs{};  // loaded by the dX waves; zero (unused) in the dS waves
+  BwdFactScalars hs{};     // loaded by the dX waves; zero (unused) in the dS waves
+  BwdFactRowScalars rsc{};  // loaded by the dS waves; zero (unused) in the dX waves
   const int te = 64 * j + 32 * (w & 1) + (threadIdx.x & 31);  // token this lane finishes (dX waves)
   // dt as used: the loaded value where the token exists and dt is given, else 1
   auto dt_use = [&](float v, int tok) { return (d.has_dt && tok < ci.len) ? v : 1.0f; };
@@ -293,7 +289,6 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
     const int xt = tid - 64 * kDsWaves;
     const int tok = 64 * j + 32 * (w & 1) + (tid & 31);
     const __amdgpu_buffer_rsrc_t rdt = buf_rsrc(d.has_dt ? a.dt + (int64_t)ci.row0 * d.H + h : csh);
-    hs.fcs = buf_ldf(rcs, (64 * j + xt) * 4, 64 * j + xt < Qpad);
     hs.ecs = buf_ldf(rcs, tok * 4, true);
     hs.edt = buf_ldf(rdt, tok * d.H * 4, d.has_dt && tok < ci.len);
     hs.cl = buf_ldf(rcs, (Qpad - 1) * 4, true);
@@ -322,6 +317,14 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
                              xrow, tv ? min(64, ci.len - 64 * (j + t)) : 0, d.P);
     }
     xt_load<PP, NP, kYThr>(YR + oS, tid, a.dst + ((int64_t)c * d.H + h) * PP * NP, NP, PP, NP);
+    const __amdgpu_buffer_rsrc_t rcs = buf_rsrc(a.cs + ((int64_t)c * d.H + h) * Qpad);
+#pragma unroll
+    for (int uu = 0; uu < kNsw; ++uu) {
+      const int row = 64 * (j + ws + kSetW * uu) + 32 * wc + (tid & 31);
+      rsc.fcs[uu] = buf_ldf(rcs, row * 4, row < Qpad);
+    }
+    rsc.cj = buf_ldf(rcs, (64 * j + 63) * 4, true);
+    rsc.fast = __float_as_int(buf_ldf(buf_rsrc(a.fast + (int64_t)c * d.H), h * 4, true));
   };
   // head order rotated per chunk: the resident blocks then read different 128-byte columns of the 8 KB
   // token rows at any moment instead of all the same one (HBM channel spread)
@@ -385,6 +388,25 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
       for (int t = 0; t < kSlots; ++t)
         if (t < nt_i) xt_store<64, PP, kYThr>(YR + TY::PER * t, tid, dyr + t * XT);
       xt_store<PP, NP, kYThr>(YR + oS, tid, dstT);
+      // f_l = exp(cs_l - c_j) of the lane's quadrant row in each tile (0 for a flagged head), and the
+      // head's S'^T = f_l S^T for the dX waves (their reads of the previous head's ended before the
+      // barrier above)
+      float fS[kNsw];
+      {
+        const bool okh = rsc.fast != 0;
+        const float cj2 = rsc.cj * SSD_LOG2E;
+#pragma unroll
+        for (int uu = 0; uu < kNsw; ++uu) {
+          const int t = ws + kSetW * uu;
+          fS[uu] = (okh && t < nt_i) ? exp2_fast(rsc.fcs[uu] * SSD_LOG2E - cj2) : 0.0f;
+          if (MODE != 2 && t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
+            const floatx16 Sq = ur_get(UR + 4 * uu);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)(Sq[v] * fS[uu]);
+          }
+        }
+      }
       lds_barrier();
       const HeadBuf hb = hbuf(k);
 
@@ -404,7 +426,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
 #pragma unroll
           for (int kk = 0; kk < PP / 16; ++kk)
             mfma(P, tld8<PP>(xu, 32 * wr + l32, 16 * kk + 8 * hh), tld8<PP>(dyt, 32 * wc + l32, 16 * kk + 8 * hh));
-          const float fl = frow[64 * t + 32 * wc + l32];
+          const float fl = fS[uu];
           const floatx16 Sq = ur_get(UR + 4 * uu);
           floatx16 dSq = ur_get(UR + 4 * (kNsw + uu));
           float G[16];
@@ -448,8 +470,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
       asm volatile("" : "+v"(tid));
       const int xt = tid - 64 * kDsWaves;
       xt_store<64, PP>(UR + oX, xt, xu);
-      // f_l of rows 64 j + xt and v_s of the head's tokens s (block j); zero for a flagged head
-      frow[xt] = (ok && xt < 64 * nt_i) ? exp2_fast(hs.fcs * SSD_LOG2E - e_cj2) : 0.0f;
+      // v_s of the head's tokens s (block j); zero for a flagged head
       if (pt == 0 && hh == 0) vrow[32 * sr + l32] = ok ? e_dt * exp2_fast(e_cj2 - e_c2) : 0.0f;
       lds_barrier();
       const HeadBuf hb = hbuf(k);
@@ -463,7 +484,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         }
         if (lane == 0) hb.d[w - kDsWaves] = 0.0f;
       } else {
-        // ---- dX^T += dy^T S' over the tiles (j + t, j), S'[l][s] = f_l S[l][s] scaled in registers;
+        // ---- dX^T += dy^T S' over the tiles (j + t, j), S'[l][s] = f_l S[l][s] as the dS waves wrote it;
         // state term dX_st^T[p][s] = sum_n dst[p][n] B[s][n] ----
         floatx16 dXa, dXs;
         zero(dXa);
@@ -474,8 +495,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           const bf16* dyt = dyr + t * XT;
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk)
-            mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane),
-                 scale8(tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh), frow + 64 * t + 16 * kk + 8 * hh));
+            mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh));
         }
 #pragma unroll
         for (int kk = 0; kk < NP / 16; ++kk)
