@@ -36,16 +36,17 @@ template <int PT, int NT>
 struct StateCfg {
   static constexpr int PP = 32 * PT;            // state rows per block
   static constexpr int NC = 32 * NT;            // state columns per block (all of Npad)
-  static constexpr int NW = PT * NT;            // waves: (p tile, n tile)
-  static constexpr int NTHR = 64 * NW;
+  static constexpr int NW = PT * NT;            // compute waves: (p tile, n tile)
+  static constexpr int NPW = 4;                 // DMA waves (one more per SIMD), after the compute waves
+  static constexpr int NTHR = 64 * (NW + NPW);
   static constexpr int R = (PT == 2 && NT == 4) ? 4 : 3;  // ring slots
   static constexpr int UB = 64 * PP * 2;        // x / dy rows of a step
   static constexpr int VB = 64 * NC * 2;        // B / C rows of a step
   static constexpr int SLOT = UB + VB + 256;    // + the step's 64 per-token factors (loaded by wave 0)
   static constexpr int UI = UB / 1024, VI = VB / 1024;  // 1 KB DMA instructions
-  static constexpr int PERW = (UI + VI) / NW;   // row DMAs per wave and step
-  static constexpr int D = PERW, D0 = PERW + 1; // DMAs per step: any wave, wave 0 (+ the factor row)
-  static_assert((UI + VI) % NW == 0, "DMA split");
+  static constexpr int PERW = (UI + VI) / NPW;  // row DMAs per DMA wave and step
+  static constexpr int D = PERW, D0 = PERW + 1; // DMAs per step: any DMA wave, DMA wave 0 (+ the factor row)
+  static_assert(UI % NPW == 0 && VI % NPW == 0, "DMA split");
   static constexpr int TP = 40;                 // s_tile row pitch (elements), 32 x 32 tiles
   // PT = 2: each wave owns all 64 p of 16 columns of the pair (four 16 x 16 MFMA tiles), so every
   // B / C element is scaled by one wave, not by both p-tile waves; other PT use 32 x 32 tiles
@@ -56,8 +57,8 @@ struct StateCfg {
   // at the chunk's end, before the next chunk's first step.
   static constexpr int TILE = TWE * 2 > 2048 ? TWE * 2 : 2048;  // bytes per wave
   static size_t bytes(bool) { return (size_t)R * SLOT + (size_t)NW * TILE; }
-  // waves per SIMD the LDS allows (one block of 16 waves at P = N = 128, else two per SIMD)
-  static constexpr int WPE = NW >= 16 ? 4 : 2;
+  // waves per SIMD a block brings (its compute waves and one DMA wave per SIMD), at least two
+  static constexpr int WPE = (NW + NPW + 3) / 4 > 2 ? (NW + NPW + 3) / 4 : 2;
 };
 
 // Whether the walk uses the 64 x 16 wave tiles: the forward walk at PT = 2. The backward walk
@@ -91,7 +92,7 @@ struct StateCtx {
   const bf16* hin_in;
   float* dtot_part;
   int64_t urow, vrow, ucol, vcol;
-  int h, w, pt, ntl, nt, NTn, c0, c1, nch;
+  int h, w, pw, pt, ntl, nt, NTn, c0, c1, nch;  // pw: index of a DMA wave
   int ncol0;  // first state column (n) of this wave's tile
   bool nt_ok;
 };
@@ -136,6 +137,17 @@ __device__ __forceinline__ void cursor_next(const StateCtx& x, Cursor& u) {
   u.ntot = chunk_total(x, cn);
 }
 
+// Advance the compute cursor past one 64-token step.
+template <bool FWD>
+__device__ __forceinline__ void cursor_step(const StateCtx& x, Cursor& u) {
+  u.t += 64;
+  if (u.t >= u.ci.len) {
+    ++u.k;
+    u.t = 0;
+    cursor_next<FWD>(x, u);
+  }
+}
+
 // The issue cursor: the walk position whose rows the next DMAs fetch, with the bases of its
 // chunk's rows (set when the cursor enters a chunk; a step's rows are then the soffset t * pitch)
 // and the next chunk's table entry (loaded a chunk ahead).
@@ -147,14 +159,13 @@ struct IssueCur {
   const float* bs;
 };
 
-// Per-wave loop invariants of the ring DMAs. Every wave issues UPW row DMAs of x / dy and VPW of
-// B / C per step (the same split in every wave, so no wave branches on its share); wave 0 also the
-// step's row of per-token factors.
+// Per-wave loop invariants of the ring DMAs. Every DMA wave issues UPW row DMAs of x / dy and VPW of
+// B / C per step (the same split in every DMA wave, so no wave branches on its share); DMA wave 0
+// also the step's row of per-token factors.
 template <int PT, int NT>
 struct IssueLanes {
   using Cfg = StateCfg<PT, NT>;
-  static constexpr int UPW = Cfg::UI / Cfg::NW, VPW = Cfg::VI / Cfg::NW;
-  static_assert(Cfg::UI % Cfg::NW == 0 && Cfg::VI % Cfg::NW == 0, "per-wave DMA split");
+  static constexpr int UPW = Cfg::UI / Cfg::NPW, VPW = Cfg::VI / Cfg::NPW;
   int ou[UPW], ov[VPW];  // lane's byte offset within the step's rows (SSD_BUF_SIZE: column outside)
   int lu[UPW], lv[VPW];  // lane's row within the step
 };
@@ -169,14 +180,14 @@ __device__ __forceinline__ IssueLanes<PT, NT> issue_lanes(const StateCtx& x, int
   IL il;
 #pragma unroll
   for (int q = 0; q < IL::UPW; ++q) {
-    const int qq = x.w * IL::UPW + q;
+    const int qq = x.pw * IL::UPW + q;
     const int r = qq * URI + lane / UG, gcol = swz_tr<PP>(r, lane % UG) << 3;
     il.lu[q] = r;
     il.ou[q] = gcol < d.P ? (int)((r * x.urow + gcol) * 2) : SSD_BUF_SIZE;
   }
 #pragma unroll
   for (int q = 0; q < IL::VPW; ++q) {
-    const int vi = x.w * IL::VPW + q;
+    const int vi = x.pw * IL::VPW + q;
     const int r = vi * VRI + lane / VG, gcol = swz_tr<NC>(r, lane % VG) << 3;
     il.lv[q] = r;
     il.ov[q] = gcol < d.N ? (int)((r * x.vrow + gcol) * 2) : SSD_BUF_SIZE;
@@ -197,7 +208,7 @@ __device__ __forceinline__ void issue_fetch(const StateCtx& x, const IssueLanes<
   u.bs = x.fac + ((int64_t)c * d.H + x.h) * d.Qpad;
 }
 
-// One step's DMAs into ring slot `nxt`: StateCfg::D per wave (D0 in wave 0), also past the
+// One step's DMAs into ring slot `nxt`: StateCfg::D per DMA wave (D0 in DMA wave 0), also past the
 // last step (then masked to zeros), so that every step issues the same count. Advances the
 // issue cursor.
 template <int PT, int NT, bool FWD>
@@ -216,15 +227,15 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
   for (int q = 0; q < IL::UPW; ++q) {
     const int vo = il.lu[q] < nrows ? il.ou[q] : SSD_BUF_SIZE;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        ru, (__attribute__((address_space(3))) void*)(nxt + (x.w * IL::UPW + q) * 1024), 16, vo, su, 0, 0);
+        ru, (__attribute__((address_space(3))) void*)(nxt + (x.pw * IL::UPW + q) * 1024), 16, vo, su, 0, 0);
   }
 #pragma unroll
   for (int q = 0; q < IL::VPW; ++q) {
     const int vo = il.lv[q] < nrows ? il.ov[q] : SSD_BUF_SIZE;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rv, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + (x.w * IL::VPW + q) * 1024), 16, vo, sv, 0, 0);
+        rv, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + (x.pw * IL::VPW + q) * 1024), 16, vo, sv, 0, 0);
   }
-  if (x.w == 0) {
+  if (x.pw == 0) {
     const int vo = lane * 4, so = t0i * 4;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, (__attribute__((address_space(3))) void*)(nxt + Cfg::UB + Cfg::VB), 4, vo, so, 0, 0);
@@ -239,10 +250,10 @@ __device__ __forceinline__ void state_issue(const StateCtx& x, const IssueLanes<
   }
 }
 
-// vmcnt wait until at most n steps' ring DMAs of this wave are outstanding (n <= 3)
+// vmcnt wait until at most n steps' ring DMAs of DMA wave pw are outstanding (n <= 3)
 template <int D0, int D>
-__device__ __forceinline__ void wait_ring(int w, int n) {
-  if (w == 0) {
+__device__ __forceinline__ void wait_ring(int pw, int n) {
+  if (pw == 0) {
     switch (n) {
       case 0: wait_vm<0>(); break;
       case 1: wait_vm<D0>(); break;
@@ -259,31 +270,24 @@ __device__ __forceinline__ void wait_ring(int w, int n) {
   }
 }
 
-// One 64-token step: refill slot `nxt`, consume slot `cur`. Every LDS access of the
-// step goes through these distinct __restrict__ pointers, which tells the compiler
-// that the new DMAs do not write what the step reads: it then adds no wait of its
-// own for them, and the slot waits stay the explicit ones of the caller.
+// One 64-token step of a compute wave: consume slot `cur` (filled by the DMA waves).
 template <int PT, int NT, bool FWD>
 __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned char* __restrict__ cur,
-                                           unsigned char* __restrict__ nxt, bf16* __restrict__ tw,
-                                           const IssueLanes<PT, NT>& il, IssueCur& ui, Cursor& uc, int& st,
-                                           int& s_start, floatx16& acc, floatx16& run) {
+                                           bf16* __restrict__ tw, Cursor& uc, floatx16& acc, floatx16& run) {
   using Cfg = StateCfg<PT, NT>;
   constexpr int PP = Cfg::PP, TP = Cfg::TP;
   constexpr bool WIDE = state_wide<PT, FWD>();
   const SsdDims& d = x.d;
   const int lane = threadIdx.x & 63;
-  state_issue<PT, NT, FWD>(x, il, nxt, ui, lane);
   const int c = uc.c;
   const int clen = uc.ci.len;
-  int& t0 = uc.t;
+  const int t0 = uc.t;
   const int64_t soff = ((int64_t)c * d.H + x.h) * d.Ppad * d.Npad;
   const int prow0 = 32 * x.pt;
   // tile geometry: rows (p) x columns (n) per wave, and the 16-byte pieces per row
   constexpr int TR = WIDE ? 64 : 32, TC = WIDE ? 16 : 32, TPR = WIDE ? Cfg::TW : TP;
   constexpr int GPR = TC / 8;
   if (t0 == 0) {
-    s_start = st;
     // state entering (forward) / gradient leaving (backward) chunk c: accumulator layout
     // -> this wave's LDS tile -> 16-byte row pieces (two per lane)
 #pragma unroll
@@ -346,16 +350,13 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
       mfma(acc, swz_tr8<PP>(tu, kk, prow0, lane), b);
     }
   }
-  t0 += 64;
-  ++st;
-  if (t0 >= clen) {
+  if (t0 + 64 >= clen) {
     // end of chunk c
     const float tot = uc.tot;
     const float dec = exp_clamp(tot);
     if (!FWD) {
-      // the h_in tile's DMAs were issued at the chunk's first step, before the ring DMAs
-      // of the (st - 1 - s_start) steps since
-      wait_ring<Cfg::D0, Cfg::D>(x.w, st - 1 - s_start);
+      // the h_in tile's DMAs (issued at the chunk's first step) are the wave's only loads
+      wait_vm<0>();
       float contrib = 0.0f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) contrib += run[v] * (float)tw[state_row<WIDE>(v, lane) * TC + state_col<WIDE>(lane)];
@@ -369,15 +370,13 @@ __device__ __forceinline__ void state_step(const StateCtx& x, const unsigned cha
 #pragma unroll
     for (int v = 0; v < 16; ++v) run[v] = dec * run[v] + acc[v];
     zero(acc);
-    ++uc.k;
-    t0 = 0;
-    cursor_next<FWD>(x, uc);
   }
+  cursor_step<FWD>(x, uc);
 }
 
-// LDS allows StateCfg::WPE waves per SIMD (two, or four for the 16-wave block at P = N = 128)
+// StateCfg::WPE waves per SIMD: the block's compute and DMA waves (one block per CU at config sizes)
 template <int PT, int NT, bool FWD>
-__global__ void __launch_bounds__(64 * PT * NT) __attribute__((amdgpu_waves_per_eu(StateCfg<PT, NT>::WPE, StateCfg<PT, NT>::WPE)))
+__global__ void __launch_bounds__((StateCfg<PT, NT>::NTHR)) __attribute__((amdgpu_waves_per_eu(StateCfg<PT, NT>::WPE, StateCfg<PT, NT>::WPE)))
 k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
                                                          const int32_t* __restrict__ seq_chunk0,
                                                          const float* __restrict__ cs, const float* __restrict__ fac,
@@ -402,6 +401,8 @@ k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
   const int sq = unit / d.H;
   const int g = x.h / d.hpg;
   x.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool dma_wave = x.w >= Cfg::NW;
+  x.pw = dma_wave ? x.w - Cfg::NW : -1;
   if constexpr (WIDE) {  // wave w: all p, columns 16 w .. 16 w + 15
     x.pt = 0;
     x.ntl = x.w >> 1;
@@ -426,9 +427,59 @@ k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
   x.ucol = (int64_t)x.h * d.P;
   x.vcol = (int64_t)g * d.N;
   const int lane = threadIdx.x & 63;
+  x.c0 = seq_chunk0[sq];
+  x.c1 = seq_chunk0[sq + 1];
+  x.nch = x.c1 - x.c0;
+  // Step st of both roles: the DMA waves wait for their DMAs of slot st % R, all waves meet at the
+  // step's barrier (step st - 1 is then done everywhere and its slot free), the DMA waves refill that
+  // slot with step st + R - 1 while the compute waves consume slot st % R. The loops are unrolled R
+  // times so that every slot address is a constant (the LDS accesses carry it in their offset field);
+  // both roles follow the same cursor, so they meet at the same number of barriers.
+  static_assert(Cfg::R == 3 || Cfg::R == 4, "three- or four-slot ring");
+  auto ring = [&](auto&& step) {
+    Cursor uc{};
+    if (x.nch > 0) cursor_init<FWD>(x, uc);
+    if constexpr (Cfg::R == 4) {
+      while (uc.k < x.nch) {
+        step(uc, smem, smem + 3 * SLOT);
+        if (uc.k >= x.nch) break;
+        step(uc, smem + SLOT, smem);
+        if (uc.k >= x.nch) break;
+        step(uc, smem + 2 * SLOT, smem + SLOT);
+        if (uc.k >= x.nch) break;
+        step(uc, smem + 3 * SLOT, smem + 2 * SLOT);
+      }
+    } else {
+      while (uc.k < x.nch) {
+        step(uc, smem, smem + 2 * SLOT);
+        if (uc.k >= x.nch) break;
+        step(uc, smem + SLOT, smem);
+        if (uc.k >= x.nch) break;
+        step(uc, smem + 2 * SLOT, smem + SLOT);
+      }
+    }
+  };
+
+  if (dma_wave) {
+    const IssueLanes<PT, NT> il = issue_lanes<PT, NT, FWD>(x, lane);
+    IssueCur ui{};  // issue cursor, R - 1 steps ahead of the compute cursor
+    if (x.nch > 0) {  // (an empty sequence passes its state through)
+      issue_fetch<PT, NT, FWD>(x, il, ui, true);
+      for (int q = 0; q < Cfg::R - 1; ++q) state_issue<PT, NT, FWD>(x, il, smem + q * SLOT, ui, lane);
+    }
+    ring([&](Cursor& uc, unsigned char* __restrict__, unsigned char* __restrict__ nxt) {
+      // this wave's DMAs of slot st are done (those of the next R - 2 slots may still fly)
+      wait_ring<Cfg::D0, Cfg::D>(x.pw, Cfg::R - 2);
+      lds_barrier();
+      state_issue<PT, NT, FWD>(x, il, nxt, ui, lane);
+      cursor_step<FWD>(x, uc);
+    });
+    wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
+    return;
+  }
+
   const int n = x.ncol0 + state_col<WIDE>(lane);
   const int prow0 = 32 * x.pt;
-
   // running state: rows p = 32 pt + acc_row(v), column n
   floatx16 run;
   zero(run);
@@ -442,52 +493,13 @@ k_state_fused(SsdDims d, const ChunkInfo* __restrict__ chunks,
       }
     }
   }
-  wait_vm<0>();  // the ring's waits below count the ring's DMAs only
-  x.c0 = seq_chunk0[sq];
-  x.c1 = seq_chunk0[sq + 1];
-  x.nch = x.c1 - x.c0;
-
-  const IssueLanes<PT, NT> il = issue_lanes<PT, NT, FWD>(x, lane);
-  IssueCur ui{};                  // issue cursor
-  Cursor uc{};                    // compute cursor
-  if (x.nch > 0) {  // (an empty sequence passes its state through)
-    issue_fetch<PT, NT, FWD>(x, il, ui, true);
-    cursor_init<FWD>(x, uc);
-    for (int q = 0; q < Cfg::R - 1; ++q) state_issue<PT, NT, FWD>(x, il, smem + q * SLOT, ui, lane);
-  }
   floatx16 acc;
   zero(acc);
-  int st = 0, s_start = 0;  // step count, step of the chunk's start
-  // step st reads slot st % R and refills slot (st + R - 1) % R; unrolled R times so that every
-  // slot address is a constant (the LDS reads carry it in their offset field)
-  static_assert(Cfg::R == 3 || Cfg::R == 4, "three- or four-slot ring");
   bf16* tw = reinterpret_cast<bf16*>(s_tile + x.w * Cfg::TILE);
-  auto step = [&](unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt) {
-    // this wave's DMAs of slot st are done (those of the next R - 2 slots may still fly)
-    wait_ring<Cfg::D0, Cfg::D>(x.w, Cfg::R - 2);
-    lds_barrier();  // ... and every wave's; step st - 1 is done everywhere, its slot free
-    state_step<PT, NT, FWD>(x, cur, nxt, tw, il, ui, uc, st, s_start, acc, run);
-  };
-  if constexpr (Cfg::R == 4) {
-    while (uc.k < x.nch) {
-      step(smem, smem + 3 * SLOT);
-      if (uc.k >= x.nch) break;
-      step(smem + SLOT, smem);
-      if (uc.k >= x.nch) break;
-      step(smem + 2 * SLOT, smem + SLOT);
-      if (uc.k >= x.nch) break;
-      step(smem + 3 * SLOT, smem + 2 * SLOT);
-    }
-  } else {
-    while (uc.k < x.nch) {
-      step(smem, smem + 2 * SLOT);
-      if (uc.k >= x.nch) break;
-      step(smem + SLOT, smem);
-      if (uc.k >= x.nch) break;
-      step(smem + 2 * SLOT, smem + SLOT);
-    }
-  }
-  wait_vm<0>();  // the trailing (masked) DMAs land before the block's LDS is released
+  ring([&](Cursor& uc, unsigned char* __restrict__ cur, unsigned char* __restrict__) {
+    lds_barrier();  // the DMA waves' loads of slot st have landed; step st - 1 is done everywhere
+    state_step<PT, NT, FWD>(x, cur, tw, uc, acc, run);
+  });
   // final state (forward) / gradient of the initial state (backward)
   if (s_out) {
 #pragma unroll
