@@ -31,9 +31,10 @@
 // for dS, rowG and colG (S^T of those two tiles kept in fp32 registers, built
 // once per block), waves 8-11 own dX^T tile (p tile (w / 2) % 2, s half w % 2)
 // over all l and finish the head's tokens. While a head is staged, the dS waves
-// write its S'^T = f_l S^T in bf16 from their fp32 quadrants (a lane's quadrant
-// column is one row l, so one factor per lane and tile), and the dX waves read it
-// as their operand; every dy row is staged once, unscaled, for both roles. Each role runs its own copy of the head
+// write its S' = f_l S in bf16 from their fp32 quadrants as [l][s] rows (a lane's
+// quadrant column is one row l, so one factor per lane and tile, and four
+// consecutive s per 8-byte store), and the dX waves read it as their operand with
+// transposed LDS reads; every dy row is staged once, unscaled, for both roles. Each role runs its own copy of the head
 // loop (two barriers per head) and loads part of the next head into registers
 // while a head computes: the dX waves the x rows and the per-token scalars
 // (before their contraction), the dS waves the dy rows and dst (after theirs,
@@ -143,6 +144,20 @@ __device__ __forceinline__ void ur_set(u32x4* R, const floatx16& f) {
     for (int e = 0; e < 4; ++e) R[q][e] = __float_as_uint(f[4 * q + e]);
 }
 
+// A dS wave's quadrant (s half wr, l half wc) of tile S (accumulator layout: lane column l, register
+// v row s = 32 wr + acc_row(v, lane)) scaled by f, into the bf16 tile t[l][s]: a lane's registers
+// 4 r .. 4 r + 3 are four consecutive s of its row l, so one 8-byte store each. With the 144-byte
+// pitch the 16 rows of a store's lane group fall on 16 different 16-byte bank slots.
+__device__ __forceinline__ void sq_store(bf16* t, const floatx16& S, float f, int wr, int wc, int L) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    bf16x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (bf16)(S[4 * r + e] * f);
+    *reinterpret_cast<bf16x4*>(t + toff<64>(32 * wc + (L & 31), 32 * wr + 8 * r + 4 * (L >> 5))) = o;
+  }
+}
+
 // Per-head scalars loaded with the next head's tiles (dX waves).
 struct BwdFactScalars {
   float ecs, edt;   // cs, dt at the token this lane finishes (64 j + 32 (w % 2) + lane % 32)
@@ -200,7 +215,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
   bf16* xu = reinterpret_cast<bf16*>(smem);  // x rows of block j          [64][PP]
   bf16* ot2 = xu + XT;                       // dx rows of block j         [2 head parity][64][PP]
   bf16* dyr = ot2 + 2 * XT;                  // dy rows of blocks j + t    [4][64][PP] (slot 0: block j)
-  bf16* St = dyr + kSlots * XT;              // S'^T tiles (j + t, j)      [4][64 s][64 l], per head
+  bf16* St = dyr + kSlots * XT;              // S' tiles (j + t, j)        [4][64 l][64 s], per head
   bf16* dstT = St + kSlots * SQ;             // dst                        [PP][NP]
   bf16* Bt = dstT + LD::DT;                  // B rows of block j          [64][NP]
   float* red = reinterpret_cast<float*>(Bt + LD::BT);
@@ -253,12 +268,9 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         }
       }
       ur_set(UR + 4 * uu, Sq);  // dS (entries 4 (kNsw + u) ..) starts at zero
-      // bf16 copy of S^T[s][l] for the dX waves: quadrants that stay zero keep it, the others are
-      // rewritten as S'^T for each head
-      if (t < kSlots) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)Sq[v];
-      }
+      // bf16 copy of S[l][s] for the dX waves: quadrants that stay zero keep it, the others are
+      // rewritten as S' for each head
+      if (t < kSlots) sq_store(St + t * SQ, Sq, 1.0f, wr, wc, lane);
     }
   }
 
@@ -352,19 +364,25 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         a.xdx[hq + tg] = b.x[tl] + b.x[64 + tl];
       }
     }
-    for (int e = tid; e < nt_i * 64; e += kFl) {
+    // compile-time trip counts (one pass at 8 dS waves): the loops unroll, no per-pass exec masks
+#pragma unroll
+    for (int q = 0; q < (kSlots * 64 + kFl - 1) / kFl; ++q) {
+      const int e = tid + q * kFl;
       const int t = e / 64, l = e % 64;
       const int lg = 64 * (j + t) + l;
-      if (lg < ci.len)
+      if (e < nt_i * 64 && lg < ci.len)
         a.rowG[((int64_t)j * d.max_chunks + c) * d.H * (int64_t)Qpad + (int64_t)h * Qpad + lg] =
             b.row[(t * 2 + 0) * 64 + l] + b.row[(t * 2 + 1) * 64 + l];
     }
     if (tid == 0) a.dD_part[((int64_t)c * d.H + h) * nb + j] = b.d[0] + b.d[1] + b.d[2] + b.d[3];
     constexpr int CPR = PP / 8;
 #pragma unroll
-    for (int id = tid; id < 64 * CPR; id += kFl) {
+    for (int q = 0; q < (64 * CPR + kFl - 1) / kFl; ++q) {
+      const int id = tid + q * kFl;
       const int r = id / CPR, kk = (id % CPR) * 8;
-      if (64 * j + r < ci.len && kk < d.P && MODE != 2)
+      // (bound kept even when the passes cover the rows exactly: the block's last flush runs on
+      // every thread, dX waves included)
+      if (id < 64 * CPR && 64 * j + r < ci.len && kk < d.P && MODE != 2)
         *reinterpret_cast<bf16x8*>(a.dx + (int64_t)(ci.row0 + 64 * j + r) * xrow + (int64_t)h * d.P + kk) =
             tld8<PP>(b.ot, r, kk);
     }
@@ -389,7 +407,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         if (t < nt_i) xt_store<64, PP, kYThr>(YR + TY::PER * t, tid, dyr + t * XT);
       xt_store<PP, NP, kYThr>(YR + oS, tid, dstT);
       // f_l = exp(cs_l - c_j) of the lane's quadrant row in each tile (0 for a flagged head), and the
-      // head's S'^T = f_l S^T for the dX waves (their reads of the previous head's ended before the
+      // head's S' = f_l S for the dX waves (their reads of the previous head's ended before the
       // barrier above)
       float fS[kNsw];
       {
@@ -399,12 +417,8 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
         for (int uu = 0; uu < kNsw; ++uu) {
           const int t = ws + kSetW * uu;
           fS[uu] = (okh && t < nt_i) ? exp2_fast(rsc.fcs[uu] * SSD_LOG2E - cj2) : 0.0f;
-          if (MODE != 2 && t < nt_i && !(t == 0 && wr == 1 && wc == 0)) {
-            const floatx16 Sq = ur_get(UR + 4 * uu);
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-              St[t * SQ + toff<64>(32 * wr + acc_row(v, lane), 32 * wc + l32)] = (bf16)(Sq[v] * fS[uu]);
-          }
+          if (MODE != 2 && t < nt_i && !(t == 0 && wr == 1 && wc == 0))
+            sq_store(St + t * SQ, ur_get(UR + 4 * uu), fS[uu], wr, wc, lane);
         }
       }
       lds_barrier();
@@ -495,7 +509,7 @@ k_bwd_fact(SsdDims d, BwdFactArgs a) {
           const bf16* dyt = dyr + t * XT;
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk)
-            mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), tld8<64>(St + t * SQ, 32 * sr + l32, 16 * kk + 8 * hh));
+            mfma(dXa, ttr_std<PP>(dyt, 16 * kk, 32 * pt, lane), ttr_std<64>(St + t * SQ, 16 * kk, 32 * sr, lane));
         }
 #pragma unroll
         for (int kk = 0; kk < NP / 16; ++kk)
