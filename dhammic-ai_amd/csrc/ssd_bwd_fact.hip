@@ -147,7 +147,8 @@ __device__ __forceinline__ void ur_set(u32x4* R, const floatx16& f) {
 // A dS wave's quadrant (s half wr, l half wc) of tile S (accumulator layout: lane column l, register
 // v row s = 32 wr + acc_row(v, lane)) scaled by f, into the bf16 tile t[l][s]: a lane's registers
 // 4 r .. 4 r + 3 are four consecutive s of its row l, so one 8-byte store each. With the 144-byte
-// pitch the 16 rows of a store's lane group fall on 16 different 16-byte bank slots.
+// pitch the 16 rows of a 16-lane group fall on 16 different 16-byte bank slots (rows l and l + 16
+// share one, so 32 lanes served together conflict 2-way).
 __device__ __forceinline__ void sq_store(bf16* t, const floatx16& S, float f, int wr, int wc, int L) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
